@@ -1,0 +1,211 @@
+/*
+ * maxsim_hip.h -- C ABI of the MI355X (gfx950) MaxSim scoring engine.
+ *
+ * Drop-in boundary for the reference's native handle module
+ * `maxsim._maxsim_cuda` (pybind11 module cpp/maxsim/cuda_extension.cu:3416-3514).
+ * Every entry point below replaces one method, property or routing knob of
+ * that module; the comment on each cites the reference line it replaces.
+ * Plain C types only: host pointers, device pointers, sizes, and an opaque
+ * HIP stream passed as void*.  No torch, no pybind, no CUDA headers.
+ *
+ * Errors: every function returns MSIM_OK or an error code and records a
+ * message readable with msim_last_error() on the calling thread.
+ * MSIM_EINVAL corresponds to the reference's std::invalid_argument
+ * (Python ValueError); MSIM_ERUNTIME to check_cuda failures (RuntimeError).
+ * A call that fails validation leaves the handle unchanged.
+ *
+ * Host-buffer methods (`const float* query` host pointers) are synchronous
+ * like the reference: they copy the query in, run, and copy results out.
+ * The *_async variants take device pointers and a stream and only enqueue.
+ * Handles are not thread-safe (the reference's per-handle workspaces are
+ * not either); use one handle per thread or serialise calls.
+ */
+#ifndef MAXSIM_HIP_H
+#define MAXSIM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSIM_OK 0
+#define MSIM_EINVAL 1
+#define MSIM_ERUNTIME 2
+#define MSIM_ENOTSUP 3
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* msim_last_error(void);
+/* ABI version (major * 100 + minor). */
+int msim_abi_version(void);
+
+/* Routing knobs: documents scored per wave by the streaming kernels
+ * (0 = automatic from the device's CU count).  Replaces the reference's
+ * launch-shape knobs set_shared_reducer_warps / set_residual_reducer_warps
+ * (cuda_extension.cu:3489-3513), whose SM89 warp shapes have no gfx950 meaning. */
+int msim_set_docs_per_wave(int value);
+int msim_get_docs_per_wave(void);
+
+/* ===================================================================== */
+/* Int4 corpus handle: CudaInt4PackedDocs (cuda_extension.cu:2677-3306). */
+/* ===================================================================== */
+typedef struct msim_int4_docs msim_int4_docs;
+
+/* CudaInt4PackedDocs.__init__(packed u8[T, dim/2], offsets i64[N+1], dim, scale)
+ * (cu:2679-2728).  Copies codes and offsets to the current device. */
+int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64_t row_bytes,
+                     const int64_t* offsets, int64_t num_offsets, int dim, double scale,
+                     msim_int4_docs** out);
+/* Destructor (cu:2733-2747). */
+int msim_int4_destroy(msim_int4_docs* h);
+/* set_token_scale_vector(f32[T]) (cu:2749-2773). */
+int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_scales, int64_t count);
+/* clear_token_scale_vector() (cu:2775). */
+int msim_int4_clear_token_scale(msim_int4_docs* h);
+/* set_residual_int4(u8[T, dim/2], scale, f32[T]) (cu:2777-2831). */
+int msim_int4_set_residual(msim_int4_docs* h, const uint8_t* packed, int64_t num_tokens,
+                           int64_t row_bytes, double scale, const float* token_scales,
+                           int64_t count);
+/* clear_residual_int4() (cu:2833). */
+int msim_int4_clear_residual(msim_int4_docs* h);
+
+/* Read-only properties dim, num_docs, num_tokens, scale, packed_size,
+ * has_token_scale_vector, token_scale_vector_size, has_residual_int4,
+ * resident_bytes, workspace_bytes (cu:3035-3055, 3496-3505). */
+typedef struct msim_int4_props {
+  int64_t dim;
+  int64_t num_docs;
+  int64_t num_tokens;
+  double scale;
+  double residual_scale;
+  uint64_t packed_size;
+  int64_t has_token_scale_vector;
+  uint64_t token_scale_vector_size;
+  int64_t has_residual_int4;
+  uint64_t resident_bytes;
+  uint64_t workspace_bytes;
+} msim_int4_props;
+int msim_int4_get_props(const msim_int4_docs* h, msim_int4_props* out);
+
+/* maxsim_batch_int8q(query f32[B,Q,128]) -> f32[B,N] (cu:2993-3006).
+ * out: host [B, N]. */
+int msim_int4_maxsim_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
+                                 int64_t query_tokens, int64_t dim, float* out);
+/* topk_batch_int8q(query, k) -> (f32[B,k], i64[B,k]) (cu:3008-3033). */
+int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
+                               int64_t query_tokens, int64_t dim, int64_t k,
+                               float* out_scores, int64_t* out_indices);
+/* Device-resident forms of the two calls above: d_query, d_out, d_scores,
+ * d_indices are device pointers; work is enqueued on `stream` (a
+ * hipStream_t, NULL = default stream) and not waited for. */
+int msim_int4_maxsim_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                 int64_t query_tokens, float* d_out, void* stream);
+int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                               int64_t query_tokens, int64_t k, float* d_scores,
+                               int64_t* d_indices, void* stream);
+
+/* Stage-level device entry points of the int8-query path (no reference
+ * counterpart; the reference fuses them inside launch_int8q_maxsim,
+ * cu:3237-3271): quantise a device query into the handle's workspace, score
+ * the last quantised query, and select top-k on device scores.  The score
+ * call must use the batch/query_tokens of the preceding quantise call. */
+int msim_int4_quantize_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                   int64_t query_tokens, void* stream);
+int msim_int4_score_int8q_async(msim_int4_docs* h, int64_t batch, int64_t query_tokens,
+                                float* d_out, void* stream);
+/* Top-k of device score rows d_scores[b * row_stride + i], i < n, ordered by
+ * (score desc, position asc); the block selector of topk_kernel (cu:1629-1692). */
+int msim_topk_async(const float* d_scores, int64_t batch, int64_t n, int64_t row_stride,
+                    int64_t k, float* d_out_scores, int64_t* d_out_indices, void* stream);
+
+/* maxsim_batch(query f32[B,Q,dim]) -> f32[B,N], fp32-query MaxSim
+ * (cu:2835-2858, kernel cu:1268-1323). */
+int msim_int4_maxsim_batch(msim_int4_docs* h, const float* query, int64_t batch,
+                           int64_t query_tokens, int64_t dim, float* out);
+/* topk_batch(query, k) (cu:2957-2991). */
+int msim_int4_topk_batch(msim_int4_docs* h, const float* query, int64_t batch,
+                         int64_t query_tokens, int64_t dim, int64_t k, float* out_scores,
+                         int64_t* out_indices);
+
+/* score_batch / score_candidates_batch / score_residual_batch /
+ * score_residual_candidates_batch (cu:2860-2955, score_impl cu:3124-3206).
+ * reducer: "maxsim" | "weighted_maxsim" | "topk2" | "topk4" | "smoothsim".
+ * weights: NULL or f32 of shape [weights_dim0] (weights_ndim 1) or
+ * [weights_dim0, weights_dim1] (weights_ndim 2), as upload_reducer_weights
+ * (cu:3080-3122) accepts.  candidates: NULL (all docs) or i64[num_candidates]
+ * shared by every batch row, output in caller order.  residual != 0 scores
+ * the fused prefix+residual similarity.  out: host [B, targets]. */
+int msim_int4_score(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                    int64_t dim, const char* reducer, const float* weights, int64_t weights_ndim,
+                    int64_t weights_dim0, int64_t weights_dim1, double temperature,
+                    const int64_t* candidates, int64_t num_candidates, int residual, float* out);
+
+/* ===================================================================== */
+/* Binary corpus handle: CudaPackedDocs (cuda_extension.cu:1872-2675).    */
+/* ===================================================================== */
+typedef struct msim_binary_docs msim_binary_docs;
+
+/* CudaPackedDocs.__init__(packed u8[T, dim/8], offsets i64[N+1], dim) (cu:1874-1917). */
+int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int64_t row_bytes,
+                       const int64_t* offsets, int64_t num_offsets, int dim,
+                       msim_binary_docs** out);
+int msim_binary_destroy(msim_binary_docs* h);
+/* set_scale_vector(f32[N]) / clear_scale_vector() (cu:1943-1956). */
+int msim_binary_set_scale_vector(msim_binary_docs* h, const float* scale, int64_t count);
+int msim_binary_clear_scale_vector(msim_binary_docs* h);
+/* set_token_scale_vector(f32[T]) / clear_token_scale_vector() (cu:1958-1973). */
+int msim_binary_set_token_scale(msim_binary_docs* h, const float* token_scales, int64_t count);
+int msim_binary_clear_token_scale(msim_binary_docs* h);
+
+typedef struct msim_binary_props {
+  int64_t dim;
+  int64_t num_docs;
+  int64_t num_tokens;
+  uint64_t packed_size;
+  int64_t has_scale_vector;
+  uint64_t scale_vector_size;
+  int64_t has_token_scale_vector;
+  uint64_t token_scale_vector_size;
+  uint64_t resident_bytes;
+  uint64_t workspace_bytes;
+} msim_binary_props;
+/* Properties (cu:2331-2347, 3437-3447). */
+int msim_binary_get_props(const msim_binary_docs* h, msim_binary_props* out);
+
+/* maxsim_batch(query f32[B,Q,dim], scale, use_scale_vector, use_token_scale)
+ * (cu:1975-2003): fp32 query x sign bits. out host [B, N]. */
+int msim_binary_maxsim_batch(msim_binary_docs* h, const float* query, int64_t batch,
+                             int64_t query_tokens, int64_t dim, double scale,
+                             int use_scale_vector, int use_token_scale, float* out);
+/* topk_batch / topk_lut_batch (cu:2069-2109, 2165-2211). */
+int msim_binary_topk_batch(msim_binary_docs* h, const float* query, int64_t batch,
+                           int64_t query_tokens, int64_t dim, int64_t k, double scale,
+                           int use_scale_vector, int use_token_scale, float* out_scores,
+                           int64_t* out_indices);
+/* score_batch / score_candidates_batch with the generalized reducers
+ * (cu:2005-2067, score_impl).  scale_vector_override: NULL or f32[N]. */
+int msim_binary_score(msim_binary_docs* h, const float* query, int64_t batch,
+                      int64_t query_tokens, int64_t dim, const char* reducer,
+                      const float* weights, int64_t weights_ndim, int64_t weights_dim0,
+                      int64_t weights_dim1, double temperature, double scale,
+                      int use_scale_vector, int use_token_scale,
+                      const float* scale_vector_override, const int64_t* candidates,
+                      int64_t num_candidates, float* out);
+/* Sign-binarised queries (XOR / popcount): qbits u8[B, Q, dim/8] in the
+ * pack_signs bit order.  Scores are sum_q max_t (dim - 2 popcount(q ^ d)),
+ * exactly what maxsim_batch returns for the +/-1 query (no reference kernel;
+ * the reference routes integer queries through topk_lut_batch, cu:2165-2211). */
+int msim_binary_hamming_batch(msim_binary_docs* h, const uint8_t* qbits, int64_t batch,
+                              int64_t query_tokens, int64_t dim, int32_t* out);
+int msim_binary_topk_hamming(msim_binary_docs* h, const uint8_t* qbits, int64_t batch,
+                             int64_t query_tokens, int64_t dim, int64_t k, float* out_scores,
+                             int64_t* out_indices);
+int msim_binary_topk_hamming_async(msim_binary_docs* h, const uint8_t* d_qbits, int64_t batch,
+                                   int64_t query_tokens, int64_t k, float* d_scores,
+                                   int64_t* d_indices, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MAXSIM_HIP_H */

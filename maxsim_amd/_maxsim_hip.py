@@ -1,0 +1,252 @@
+"""Resident-corpus device handles over the C ABI (libmaxsim_hip.so).
+
+This module is the MI355X replacement for the reference's native handle
+module ``maxsim._maxsim_cuda`` (pybind11, cpp/maxsim/cuda_extension.cu:3416-3514).
+Class names, method names, argument order, defaults, return shapes and error
+types/messages follow that module so that the reference's Python layer
+(which probes it with ``hasattr``/``getattr``) and code written against it can
+use these handles unchanged.  Arrays are accepted the way pybind11's
+``array_t<T, c_style | forcecast>`` accepts them: anything NumPy can convert,
+copied to a C-contiguous array of the target dtype.
+
+Every scoring call runs on the GPU through HIP kernels; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from maxsim_amd import _native
+from maxsim_amd._native import check, ptr
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def _i64(a):
+    return np.ascontiguousarray(a, dtype=np.int64)
+
+
+def _query3(query):
+    q = _f32(query)
+    if q.ndim != 3:
+        raise ValueError("query must have shape [batch, query_tokens, dim]")
+    return q
+
+
+def _weights(query_weights):
+    """(array, ndim, dim0, dim1) for the C ABI's reducer weights."""
+    if query_weights is None:
+        return None, 0, 0, 0
+    try:
+        w = np.ascontiguousarray(query_weights, dtype=np.float32)
+    except (TypeError, ValueError) as exc:
+        raise ValueError("query_weights must be convertible to a float32 array") from exc
+    if w.ndim == 1:
+        return w, 1, w.shape[0], 0
+    if w.ndim == 2:
+        return w, 2, w.shape[0], w.shape[1]
+    raise ValueError("query_weights must have shape [query_tokens] or [batch, query_tokens]")
+
+
+def _candidates(candidate_indices):
+    c = _i64(candidate_indices)
+    if c.ndim != 1:
+        raise ValueError("candidate_indices must be a 1-D array")
+    return c
+
+
+def set_docs_per_wave(value: int) -> None:
+    """Routing knob: documents per wave of the streaming kernels (0 = auto)."""
+    check(_native.load().msim_set_docs_per_wave(int(value)))
+
+
+def get_docs_per_wave() -> int:
+    return int(_native.load().msim_get_docs_per_wave())
+
+
+class CudaInt4PackedDocs:
+    """Resident int4 corpus (reference: CudaInt4PackedDocs, cu:2677-3306)."""
+
+    def __init__(self, packed, offsets, dim: int, scale: float):
+        lib = _native.load()
+        packed = _u8(packed)
+        offsets = _i64(offsets)
+        if packed.ndim != 2:
+            raise ValueError("packed must have shape [num_doc_tokens, dim / 2]")
+        if offsets.ndim != 1:
+            raise ValueError("offsets must be a 1-D array")
+        handle = ctypes.c_void_p()
+        check(lib.msim_int4_create(ptr(packed), packed.shape[0], packed.shape[1], ptr(offsets),
+                                   offsets.shape[0], int(dim), float(scale), ctypes.byref(handle)))
+        self._lib = lib
+        self._h = handle
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.msim_int4_destroy(h)
+            self._h = None
+
+    # ---------------------------------------------------------- residency
+    def set_token_scale_vector(self, token_scales):
+        ts = _f32(token_scales)
+        if ts.ndim != 1:
+            raise ValueError("token scale vector must have shape [num_doc_tokens]")
+        check(self._lib.msim_int4_set_token_scale(self._h, ptr(ts), ts.shape[0]))
+
+    def clear_token_scale_vector(self):
+        check(self._lib.msim_int4_clear_token_scale(self._h))
+
+    def set_residual_int4(self, packed, scale, token_scales):
+        p = _u8(packed)
+        ts = _f32(token_scales)
+        if p.ndim != 2:
+            raise ValueError("residual packed data must have shape [num_doc_tokens, dim / 2]")
+        if ts.ndim != 1:
+            raise ValueError("residual token scale vector must have shape [num_doc_tokens]")
+        check(self._lib.msim_int4_set_residual(self._h, ptr(p), p.shape[0], p.shape[1], float(scale),
+                                               ptr(ts), ts.shape[0]))
+
+    def clear_residual_int4(self):
+        check(self._lib.msim_int4_clear_residual(self._h))
+
+    # ------------------------------------------------------------ scoring
+    def maxsim_batch(self, query):
+        q = _query3(query)
+        out = np.empty((q.shape[0], self.num_docs), np.float32)
+        check(self._lib.msim_int4_maxsim_batch(self._h, ptr(q), *q.shape, ptr(out)))
+        return out
+
+    def topk_batch(self, query, k):
+        q = _query3(query)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(self._lib.msim_int4_topk_batch(self._h, ptr(q), *q.shape, k, ptr(scores), ptr(indices)))
+        return scores, indices
+
+    def maxsim_batch_int8q(self, query):
+        q = _query3(query)
+        out = np.empty((q.shape[0], self.num_docs), np.float32)
+        check(self._lib.msim_int4_maxsim_batch_int8q(self._h, ptr(q), *q.shape, ptr(out)))
+        return out
+
+    def topk_batch_int8q(self, query, k):
+        q = _query3(query)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(self._lib.msim_int4_topk_batch_int8q(self._h, ptr(q), *q.shape, k, ptr(scores),
+                                                   ptr(indices)))
+        return scores, indices
+
+    def _score(self, query, candidate_indices, reducer, query_weights, temperature, residual):
+        q = _query3(query)
+        w, wnd, w0, w1 = _weights(query_weights)
+        cand = None if candidate_indices is None else _candidates(candidate_indices)
+        targets = self.num_docs if cand is None else cand.shape[0]
+        out = np.empty((q.shape[0], targets), np.float32)
+        if not isinstance(reducer, str):
+            raise ValueError("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'")
+        check(self._lib.msim_int4_score(
+            self._h, ptr(q), *q.shape, reducer.encode(), ptr(w), wnd, w0, w1, float(temperature),
+            ptr(cand), 0 if cand is None else cand.shape[0], 1 if residual else 0, ptr(out)))
+        return out
+
+    def score_batch(self, query, reducer="maxsim", query_weights=None, temperature=1.0):
+        return self._score(query, None, reducer, query_weights, temperature, False)
+
+    def score_candidates_batch(self, query, candidate_indices, reducer="maxsim", query_weights=None,
+                               temperature=1.0):
+        return self._score(query, candidate_indices, reducer, query_weights, temperature, False)
+
+    def score_residual_batch(self, query, reducer="maxsim", query_weights=None, temperature=1.0):
+        return self._score(query, None, reducer, query_weights, temperature, True)
+
+    def score_residual_candidates_batch(self, query, candidate_indices, reducer="maxsim",
+                                        query_weights=None, temperature=1.0):
+        return self._score(query, candidate_indices, reducer, query_weights, temperature, True)
+
+    # ------------------------------------------------- device-resident (torch)
+    def maxsim_int8q_async(self, query, out, stream=None):
+        """Enqueue int8-query MaxSim on device tensors: query f32[B,Q,128] and
+        out f32[B,N] (torch tensors on this handle's device, contiguous)."""
+        b, q = int(query.shape[0]), int(query.shape[1])
+        check(self._lib.msim_int4_maxsim_int8q_async(self._h, ptr(query), b, q, ptr(out),
+                                                     _stream_ptr(stream)))
+
+    def topk_int8q_async(self, query, k, scores, indices, stream=None):
+        """Enqueue int8-query MaxSim + top-k on device tensors (scores f32[B,k],
+        indices i64[B,k])."""
+        b, q = int(query.shape[0]), int(query.shape[1])
+        check(self._lib.msim_int4_topk_int8q_async(self._h, ptr(query), b, q, int(k), ptr(scores),
+                                                   ptr(indices), _stream_ptr(stream)))
+
+    # --------------------------------------------------------- properties
+    def _props(self):
+        props = _native.Int4Props()
+        check(self._lib.msim_int4_get_props(self._h, ctypes.byref(props)))
+        return props
+
+    @property
+    def dim(self) -> int:
+        return int(self._props().dim)
+
+    @property
+    def num_docs(self) -> int:
+        return int(self._props().num_docs)
+
+    @property
+    def num_tokens(self) -> int:
+        return int(self._props().num_tokens)
+
+    @property
+    def scale(self) -> float:
+        return float(np.float32(self._props().scale))
+
+    @property
+    def packed_size(self) -> int:
+        return int(self._props().packed_size)
+
+    @property
+    def has_token_scale_vector(self) -> bool:
+        return bool(self._props().has_token_scale_vector)
+
+    @property
+    def token_scale_vector_size(self) -> int:
+        return int(self._props().token_scale_vector_size)
+
+    @property
+    def has_residual_int4(self) -> bool:
+        return bool(self._props().has_residual_int4)
+
+    @property
+    def resident_bytes(self) -> int:
+        return int(self._props().resident_bytes)
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(self._props().workspace_bytes)
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        try:
+            import torch
+
+            return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        except Exception:  # pragma: no cover - torch absent
+            return None
+    handle = getattr(stream, "cuda_stream", stream)
+    return ctypes.c_void_p(int(handle))

@@ -1,0 +1,448 @@
+// capi.cpp -- C ABI (include/maxsim_hip.h): resident corpus handles,
+// input validation with the reference's messages, device workspaces and
+// kernel orchestration.  Handle semantics follow CudaInt4PackedDocs
+// (cuda_extension.cu:2677-3306) and CudaPackedDocs (cu:1872-2675).
+#include "capi_internal.hpp"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+namespace msim {
+
+thread_local std::string g_last_error;
+int g_docs_per_wave = 0;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw RuntimeError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+DeviceBuffer::~DeviceBuffer() {
+  if (ptr) (void)hipFree(ptr);
+}
+
+void DeviceBuffer::ensure(size_t bytes, const char* what) {
+  if (bytes <= cap) return;
+  void* next = nullptr;
+  check_hip(hipMalloc(&next, bytes), what);
+  if (ptr) (void)hipFree(ptr);
+  ptr = next;
+  cap = bytes;
+}
+
+void DeviceBuffer::reset() {
+  if (ptr) (void)hipFree(ptr);
+  ptr = nullptr;
+  cap = 0;
+}
+
+void validate_offsets(const int64_t* offsets, int64_t count, int64_t num_tokens) {
+  if (offsets == nullptr || count < 2) throw InvalidArgument("offsets must contain at least [0, num_doc_tokens]");
+  if (offsets[0] != 0) throw InvalidArgument("offsets must start at 0");
+  if (offsets[count - 1] != num_tokens) throw InvalidArgument("offsets must end at num_doc_tokens");
+  for (int64_t i = 1; i < count; ++i)
+    if (offsets[i] < offsets[i - 1]) throw InvalidArgument("offsets must be monotonically nondecreasing");
+}
+
+void validate_positive_scales(const float* v, int64_t n, const char* msg) {
+  for (int64_t i = 0; i < n; ++i)
+    if (!(v[i] > 0.0f) || !std::isfinite(v[i])) throw InvalidArgument(msg);
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+int32_t docs_per_wave_for(int64_t num_docs, int waves_per_cu) {
+  if (g_docs_per_wave > 0) return g_docs_per_wave;
+  const int64_t target = (int64_t)device_cu_count() * waves_per_cu;
+  int64_t dpw = (num_docs + target - 1) / target;
+  return (int32_t)(dpw < 1 ? 1 : dpw);
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace msim
+
+using namespace msim;
+
+// ------------------------------------------------------------------ global
+
+extern "C" const char* msim_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int msim_abi_version(void) { return 100; }
+
+extern "C" int msim_set_docs_per_wave(int value) {
+  return guarded([&] {
+    if (value < 0) throw InvalidArgument("docs per wave must be >= 0 (0 = automatic)");
+    g_docs_per_wave = value;
+  });
+}
+
+extern "C" int msim_get_docs_per_wave(void) { return g_docs_per_wave; }
+
+// -------------------------------------------------------------- int4 handle
+
+struct msim_int4_docs {
+  int device = 0;
+  int64_t dim = 0;
+  int64_t num_docs = 0;
+  int64_t num_tokens = 0;
+  double scale = 1.0;
+  double residual_scale = 1.0;
+  uint64_t packed_size = 0;
+  uint64_t offsets_size = 0;
+  bool has_token_scale = false;
+  bool has_residual = false;
+  int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
+  DeviceBuffer packed, offsets, token_scales, residual_packed, residual_token_scales;
+  // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
+  DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax, weights,
+      candidates;
+
+  uint64_t resident_bytes() const {
+    return packed_size + offsets_size * 8 + token_scales.cap + residual_packed.cap +
+           residual_token_scales.cap;
+  }
+  uint64_t workspace_bytes() const {
+    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap +
+           top_indices.cap + rowmax.cap + weights.cap + candidates.cap;
+  }
+};
+
+namespace {
+
+void select_device(int device) { check_hip(hipSetDevice(device), "hipSetDevice"); }
+
+void check_query_dim(int64_t dim, int64_t expected) {
+  if (dim != expected) throw InvalidArgument("query shape does not match dim");
+}
+
+void check_k(int64_t k, int64_t num_docs) {
+  if (k < 1 || k > num_docs) throw InvalidArgument("k must be between 1 and num_docs");
+  if (k > kTopkMaxK) throw NotSupported("k above 4096 is not supported by the device top-k selector");
+}
+
+void check_int8q(const msim_int4_docs* h) {
+  if (h->dim != 128) throw InvalidArgument("int8 query scoring currently requires dim=128");
+}
+
+// Quantise d_query [B,Q,128] into the handle's query workspace.
+void quantize_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
+                    hipStream_t stream) {
+  const int64_t rows = batch * query_tokens;
+  h->quantized_rows = -1;
+  if (rows == 0) return;
+  // Passes read up to 15 rows past their last valid row; pad so they stay in bounds.
+  const int64_t rows_padded = ((rows + 15) / 16) * 16 + 16;
+  h->qpack.ensure(rows_padded * 128, "hipMalloc int8q query codes");
+  h->qscale.ensure(rows_padded * 4, "hipMalloc int8q query scales");
+  h->qbias.ensure(rows_padded * 4, "hipMalloc int8q query bias");
+  check_hip(launch_quantize_int8(d_query, rows, rows_padded, h->qpack.as<int8_t>(),
+                                 h->qscale.as<float>(), h->qbias.as<int32_t>(), stream),
+            "launch int8 query quantize kernel");
+  h->quantized_rows = rows;
+}
+
+// Score the quantised query in the workspace against every document: d_out [B, N].
+void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* d_out,
+                 hipStream_t stream) {
+  const int64_t rows = batch * query_tokens;
+  if (rows == 0 || h->num_docs == 0) {
+    if (batch > 0 && h->num_docs > 0)
+      check_hip(launch_fill_f32(d_out, batch * h->num_docs, 0.0f, stream), "zero scores");
+    return;
+  }
+  if (h->quantized_rows != rows)
+    throw InvalidArgument("no quantised query of this shape: call quantize first with the same batch and query_tokens");
+  int8_t* qpack = h->qpack.as<int8_t>();
+  float* qscale = h->qscale.as<float>();
+  int32_t* qbias = h->qbias.as<int32_t>();
+
+  Int8qArgs a{};
+  a.codes = h->packed.as<uint8_t>();
+  a.token_scale = h->has_token_scale ? h->token_scales.as<float>() : nullptr;
+  a.offsets = h->offsets.as<int64_t>();
+  a.num_tokens = h->num_tokens;
+  a.num_docs = h->num_docs;
+  a.docs_per_wave = docs_per_wave_for(h->num_docs, 8);
+  a.query_tokens = (int32_t)query_tokens;
+  a.scale = h->scale;
+  a.out_stride = h->num_docs;
+  if (query_tokens <= 128) {
+    const int64_t per_pass = 128 / query_tokens;
+    for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
+      const int64_t nb = std::min(per_pass, batch - b0);
+      a.qpack = qpack + b0 * query_tokens * 128;
+      a.qscale = qscale + b0 * query_tokens;
+      a.qbias = qbias + b0 * query_tokens;
+      a.batch = (int32_t)nb;
+      a.out = d_out + b0 * h->num_docs;
+      a.rowmax_out = nullptr;
+      a.rows_valid = (int32_t)(nb * query_tokens);
+      check_hip(launch_int8q_maxsim(a, (int)(nb * query_tokens), h->has_token_scale, true, stream),
+                "launch int4 int8q maxsim kernel");
+    }
+  } else {
+    h->rowmax.ensure(sizeof(float) * rows * h->num_docs, "hipMalloc int8q row maxima");
+    float* rowmax = h->rowmax.as<float>();
+    for (int64_t r0 = 0; r0 < rows; r0 += 128) {
+      const int64_t nr = std::min<int64_t>(128, rows - r0);
+      a.qpack = qpack + r0 * 128;
+      a.qscale = qscale + r0;
+      a.qbias = qbias + r0;
+      a.batch = 0;
+      a.out = nullptr;
+      a.rowmax_out = rowmax + r0 * h->num_docs;
+      a.rows_valid = (int32_t)nr;
+      check_hip(launch_int8q_maxsim(a, (int)nr, h->has_token_scale, false, stream),
+                "launch int4 int8q maxsim kernel");
+    }
+    check_hip(launch_int8q_finish(rowmax, qscale, batch, query_tokens, h->num_docs, h->scale,
+                                  h->offsets.as<int64_t>(), d_out, stream),
+              "launch int8q finish kernel");
+  }
+}
+
+void run_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
+               float* d_out, hipStream_t stream) {
+  quantize_int8q(h, d_query, batch, query_tokens, stream);
+  score_int8q(h, batch, query_tokens, d_out, stream);
+}
+
+float* ensure_scores(msim_int4_docs* h, int64_t batch, int64_t targets) {
+  h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
+  return h->scores.as<float>();
+}
+
+float* upload_query(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                    int64_t dim, hipStream_t stream) {
+  const size_t bytes = sizeof(float) * (size_t)(batch * query_tokens * dim);
+  h->query.ensure(std::max<size_t>(bytes, 4), "hipMalloc query cache");
+  if (bytes) check_hip(hipMemcpyAsync(h->query.ptr, query, bytes, hipMemcpyHostToDevice, stream), "copy query to device");
+  return h->query.as<float>();
+}
+
+}  // namespace
+
+extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64_t row_bytes,
+                                const int64_t* offsets, int64_t num_offsets, int dim, double scale,
+                                msim_int4_docs** out) {
+  return guarded([&] {
+    if (out == nullptr) throw InvalidArgument("out handle pointer must not be NULL");
+    *out = nullptr;
+    if (dim <= 0 || dim % 2 != 0) throw InvalidArgument("dim must be positive and divisible by 2");
+    if (row_bytes != dim / 2) throw InvalidArgument("packed shape does not match dim");
+    if (num_tokens < 0) throw InvalidArgument("packed must have shape [num_doc_tokens, dim / 2]");
+    if (num_offsets < 2) throw InvalidArgument("offsets must contain at least [0, num_doc_tokens]");
+    if (!(scale > 0.0) || !std::isfinite(scale)) throw InvalidArgument("scale must be finite and > 0");
+    validate_offsets(offsets, num_offsets, num_tokens);
+    if (num_tokens > 0 && packed == nullptr) throw InvalidArgument("packed must not be NULL");
+    auto h = std::make_unique<msim_int4_docs>();
+    check_hip(hipGetDevice(&h->device), "hipGetDevice");
+    h->dim = dim;
+    h->num_docs = num_offsets - 1;
+    h->num_tokens = num_tokens;
+    h->scale = scale;
+    h->packed_size = (uint64_t)num_tokens * (uint64_t)row_bytes;
+    h->offsets_size = (uint64_t)num_offsets;
+    h->packed.ensure(std::max<uint64_t>(h->packed_size, 64), "hipMalloc int4 packed docs");
+    h->offsets.ensure(h->offsets_size * 8, "hipMalloc int4 offsets");
+    if (h->packed_size)
+      check_hip(hipMemcpy(h->packed.ptr, packed, h->packed_size, hipMemcpyHostToDevice), "copy int4 packed docs to device");
+    check_hip(hipMemcpy(h->offsets.ptr, offsets, h->offsets_size * 8, hipMemcpyHostToDevice), "copy int4 offsets to device");
+    *out = h.release();
+  });
+}
+
+extern "C" int msim_int4_destroy(msim_int4_docs* h) {
+  return guarded([&] {
+    if (h == nullptr) return;
+    (void)hipSetDevice(h->device);
+    delete h;
+  });
+}
+
+extern "C" int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_scales, int64_t count) {
+  return guarded([&] {
+    require_handle(h);
+    if (count != h->num_tokens) throw InvalidArgument("token scale vector must have shape [num_doc_tokens]");
+    validate_positive_scales(token_scales, count, "token scales must be finite and > 0");
+    select_device(h->device);
+    h->token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector");
+    if (count)
+      check_hip(hipMemcpy(h->token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 token scale vector to device");
+    h->has_token_scale = true;
+  });
+}
+
+extern "C" int msim_int4_clear_token_scale(msim_int4_docs* h) {
+  return guarded([&] {
+    require_handle(h);
+    h->has_token_scale = false;
+  });
+}
+
+extern "C" int msim_int4_set_residual(msim_int4_docs* h, const uint8_t* packed, int64_t num_tokens,
+                                      int64_t row_bytes, double scale, const float* token_scales,
+                                      int64_t count) {
+  return guarded([&] {
+    require_handle(h);
+    if (num_tokens != h->num_tokens || row_bytes != h->dim / 2)
+      throw InvalidArgument("residual packed data must have shape [num_doc_tokens, dim / 2]");
+    if (!(scale > 0.0) || !std::isfinite(scale)) throw InvalidArgument("residual scale must be finite and > 0");
+    if (count != h->num_tokens) throw InvalidArgument("residual token scale vector must have shape [num_doc_tokens]");
+    validate_positive_scales(token_scales, count, "residual token scales must be finite and > 0");
+    select_device(h->device);
+    const size_t pbytes = (size_t)num_tokens * (size_t)row_bytes;
+    h->residual_packed.ensure(std::max<size_t>(pbytes, 64), "hipMalloc resident int4 residual data");
+    h->residual_token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 residual token scales");
+    if (pbytes) check_hip(hipMemcpy(h->residual_packed.ptr, packed, pbytes, hipMemcpyHostToDevice), "copy int4 residual data to device");
+    if (count) check_hip(hipMemcpy(h->residual_token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 residual token scales to device");
+    h->residual_scale = scale;
+    h->has_residual = true;
+  });
+}
+
+extern "C" int msim_int4_clear_residual(msim_int4_docs* h) {
+  return guarded([&] {
+    require_handle(h);
+    h->has_residual = false;
+  });
+}
+
+extern "C" int msim_int4_get_props(const msim_int4_docs* h, msim_int4_props* out) {
+  return guarded([&] {
+    require_handle(h);
+    if (out == nullptr) throw InvalidArgument("props pointer must not be NULL");
+    out->dim = h->dim;
+    out->num_docs = h->num_docs;
+    out->num_tokens = h->num_tokens;
+    out->scale = h->scale;
+    out->residual_scale = h->residual_scale;
+    out->packed_size = h->packed_size;
+    out->has_token_scale_vector = h->has_token_scale ? 1 : 0;
+    out->token_scale_vector_size = h->has_token_scale ? (uint64_t)h->num_tokens : 0;
+    out->has_residual_int4 = h->has_residual ? 1 : 0;
+    out->resident_bytes = h->resident_bytes();
+    out->workspace_bytes = h->workspace_bytes();
+  });
+}
+
+extern "C" int msim_int4_maxsim_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
+                                            int64_t query_tokens, int64_t dim, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_int8q(h);
+    check_query_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    hipStream_t stream = nullptr;
+    float* d_query = upload_query(h, query, batch, query_tokens, dim, stream);
+    float* d_scores = ensure_scores(h, batch, h->num_docs);
+    run_int8q(h, d_query, batch, query_tokens, d_scores, stream);
+    check_hip(hipMemcpyAsync(out, d_scores, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost, stream), "copy int8q output to host");
+    check_hip(hipStreamSynchronize(stream), "synchronize int4 int8q maxsim");
+  });
+}
+
+extern "C" int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
+                                          int64_t query_tokens, int64_t dim, int64_t k,
+                                          float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_int8q(h);
+    check_query_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    select_device(h->device);
+    hipStream_t stream = nullptr;
+    float* d_query = upload_query(h, query, batch, query_tokens, dim, stream);
+    float* d_scores = ensure_scores(h, batch, h->num_docs);
+    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc int8q top score cache");
+    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc int8q top index cache");
+    run_int8q(h, d_query, batch, query_tokens, d_scores, stream);
+    check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr,
+                          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), stream),
+              "launch int8q topk selection kernel");
+    check_hip(hipMemcpyAsync(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top scores to host");
+    check_hip(hipMemcpyAsync(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top indices to host");
+    check_hip(hipStreamSynchronize(stream), "synchronize int8q topk kernels");
+  });
+}
+
+extern "C" int msim_int4_maxsim_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                            int64_t query_tokens, float* d_out, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_int8q(h);
+    require_shape(batch, query_tokens);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    run_int8q(h, d_query, batch, query_tokens, d_out, as_stream(stream));
+  });
+}
+
+extern "C" int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                          int64_t query_tokens, int64_t k, float* d_scores,
+                                          int64_t* d_indices, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_int8q(h);
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    select_device(h->device);
+    float* d_full = ensure_scores(h, batch, h->num_docs);
+    run_int8q(h, d_query, batch, query_tokens, d_full, as_stream(stream));
+    check_hip(launch_topk(d_full, batch, h->num_docs, h->num_docs, k, nullptr, d_scores, d_indices,
+                          as_stream(stream)),
+              "launch int8q topk selection kernel");
+  });
+}
+
+extern "C" int msim_int4_quantize_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                              int64_t query_tokens, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_int8q(h);
+    require_shape(batch, query_tokens);
+    select_device(h->device);
+    quantize_int8q(h, d_query, batch, query_tokens, as_stream(stream));
+  });
+}
+
+extern "C" int msim_int4_score_int8q_async(msim_int4_docs* h, int64_t batch, int64_t query_tokens,
+                                           float* d_out, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_int8q(h);
+    require_shape(batch, query_tokens);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    score_int8q(h, batch, query_tokens, d_out, as_stream(stream));
+  });
+}
+
+extern "C" int msim_topk_async(const float* d_scores, int64_t batch, int64_t n, int64_t row_stride,
+                               int64_t k, float* d_out_scores, int64_t* d_out_indices, void* stream) {
+  return guarded([&] {
+    if (batch < 0 || n < 0) throw InvalidArgument("scores must have shape [batch, n]");
+    if (row_stride < n) throw InvalidArgument("row_stride must be >= n");
+    check_k(k, n);
+    if (batch == 0) return;
+    check_hip(launch_topk(d_scores, batch, n, row_stride, k, nullptr, d_out_scores, d_out_indices,
+                          as_stream(stream)),
+              "launch topk selection kernel");
+  });
+}

@@ -1,0 +1,104 @@
+// common.hpp -- device helpers shared by the MI355X (gfx950) MaxSim kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace msim {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// gfx9 buffer descriptor word 3 (raw byte addressing, bounds-checked by
+// num_records: out-of-range lanes read zero instead of faulting).
+constexpr int kBufferFlags = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, kBufferFlags);
+}
+
+__device__ __forceinline__ v4u load_b128(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0);
+}
+
+__device__ __forceinline__ unsigned load_b32(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 0);
+}
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(a, fmaxf(b, c)); }
+
+// numpy's pairwise float64 reduction order over a[0..n) for 8 < n <= 128 is
+// eight strided accumulators, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),
+// then the n % 8 tail added sequentially; below 8 it is a plain sequential
+// sum from 0.0; above 128 it splits at n/2 rounded down to a multiple of 8.
+// pairwise_sum_serial evaluates that exact tree on one lane.  `get(i)`
+// returns a[i] as double.
+template <typename Get>
+__device__ double pairwise_block(Get get, int64_t base, int64_t n) {
+  if (n < 8) {
+    double res = 0.0;
+    for (int64_t i = 0; i < n; ++i) res = __dadd_rn(res, get(base + i));
+    return res;
+  }
+  double r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = get(base + j);
+  int64_t i = 8;
+  for (; i < n - (n % 8); i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = __dadd_rn(r[j], get(base + i + j));
+  }
+  double res = __dadd_rn(__dadd_rn(__dadd_rn(r[0], r[1]), __dadd_rn(r[2], r[3])),
+                         __dadd_rn(__dadd_rn(r[4], r[5]), __dadd_rn(r[6], r[7])));
+  for (; i < n; ++i) res = __dadd_rn(res, get(base + i));
+  return res;
+}
+
+template <typename Get>
+__device__ double pairwise_sum_serial(Get get, int64_t n) {
+  if (n <= 128) return pairwise_block(get, 0, n);
+  // Iterative post-order walk of numpy's split tree.
+  struct Frame {
+    int64_t base, n;
+    int state;
+    double left;
+  };
+  Frame stack[40];
+  int top = 0;
+  stack[0] = {0, n, 0, 0.0};
+  double ret = 0.0;
+  while (top >= 0) {
+    Frame& f = stack[top];
+    if (f.n <= 128) {
+      ret = pairwise_block(get, f.base, f.n);
+      --top;
+      continue;
+    }
+    int64_t n2 = f.n / 2;
+    n2 -= n2 % 8;
+    if (f.state == 0) {
+      f.state = 1;
+      stack[top + 1] = {f.base, n2, 0, 0.0};
+      ++top;
+    } else if (f.state == 1) {
+      f.left = ret;
+      f.state = 2;
+      stack[top + 1] = {f.base + n2, f.n - n2, 0, 0.0};
+      ++top;
+    } else {
+      ret = __dadd_rn(f.left, ret);
+      --top;
+    }
+  }
+  return ret;
+}
+
+}  // namespace msim
