@@ -25,6 +25,11 @@ FLAGS = [
     # Every float operation is the single rounding it reads as.
     "-ffp-contract=off",
     "-fno-gpu-rdc",
+    # MFMA results in VGPRs: the epilogue reads them directly (no accvgpr moves).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # Device code never produces or tests NaNs: fmaxf needs no operand
+    # canonicalisation (host code keeps IEEE NaN semantics for validation).
+    "-Xarch_device", "-fno-honor-nans",
     "-Wall",
     "-Wno-unused-result",
 ]

@@ -8,6 +8,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <vector>
 
 namespace msim {
 
@@ -103,6 +104,9 @@ struct msim_int4_docs {
   bool has_token_scale = false;
   bool has_residual = false;
   int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
+  std::vector<int64_t> host_offsets;
+  int64_t partition_waves = 0;    // wave count the cached partition was built for
+  DeviceBuffer wave_docs, counter;
   DeviceBuffer packed, offsets, token_scales, residual_packed, residual_token_scales;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax, weights,
@@ -114,7 +118,7 @@ struct msim_int4_docs {
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap +
-           top_indices.cap + rowmax.cap + weights.cap + candidates.cap;
+           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_docs.cap + counter.cap;
   }
 };
 
@@ -212,10 +216,93 @@ void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* 
   }
 }
 
+// Contiguous document ranges for `waves` waves, balanced by cost
+// ceil(len / 16) + 1 (16-token tiles plus the per-document finish).
+void build_partition(msim_int4_docs* h, int64_t waves) {
+  if (h->partition_waves == waves) return;
+  const int64_t n = h->num_docs;
+  std::vector<int64_t> cost(n + 1, 0);
+  for (int64_t d = 0; d < n; ++d) {
+    const int64_t len = h->host_offsets[d + 1] - h->host_offsets[d];
+    cost[d + 1] = cost[d] + (len + 15) / 16 + 1;
+  }
+  std::vector<int64_t> part(waves + 1);
+  for (int64_t w = 0; w <= waves; ++w) {
+    const int64_t target = w == waves ? cost[n] + 1 : (cost[n] * w) / waves;
+    part[w] = std::lower_bound(cost.begin(), cost.end(), target) - cost.begin();
+    part[w] = std::min(part[w], n);
+  }
+  part[0] = 0;
+  part[waves] = n;
+  h->wave_docs.ensure(sizeof(int64_t) * (waves + 1), "hipMalloc wave partition");
+  check_hip(hipMemcpy(h->wave_docs.ptr, part.data(), sizeof(int64_t) * (waves + 1), hipMemcpyHostToDevice),
+            "copy wave partition to device");
+  h->partition_waves = waves;
+}
+
+int64_t search_waves(const msim_int4_docs* h) {
+  // Default: two resident workgroups of fused_waves_per_block() waves per CU.
+  int64_t waves = g_docs_per_wave > 0 ? (h->num_docs + g_docs_per_wave - 1) / g_docs_per_wave
+                                      : (int64_t)device_cu_count() * 2 * fused_waves_per_block();
+  waves = std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
+  return waves;
+}
+
+uint32_t* ticket_counter(msim_int4_docs* h) {
+  if (h->counter.cap == 0) {
+    h->counter.ensure(256, "hipMalloc top-k ticket");
+    check_hip(hipMemset(h->counter.ptr, 0, 256), "zero top-k ticket");
+  }
+  return h->counter.as<uint32_t>();
+}
+
+// Full int8-query search: scores of every document into d_scores [B, N] and,
+// when k > 0, the top-k of each batch row into d_top_s / d_top_i [B, k].
+void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
+                  float* d_scores, int64_t k, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
+  if (batch == 0) return;
+  const bool fused = query_tokens > 0 && query_tokens <= 128 && h->num_docs > 0;
+  if (!fused) {
+    quantize_int8q(h, d_query, batch, query_tokens, stream);
+    score_int8q(h, batch, query_tokens, d_scores, stream);
+    if (k > 0)
+      check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),
+                "launch int8q topk selection kernel");
+    return;
+  }
+  const int64_t waves = search_waves(h);
+  build_partition(h, waves);
+  const bool fused_topk = k > 0 && k <= kFusedMaxK && h->num_docs <= kFusedTailMaxDocs;
+  FusedArgs a{};
+  a.codes = h->packed.as<uint8_t>();
+  a.token_scale = h->has_token_scale ? h->token_scales.as<float>() : nullptr;
+  a.offsets = h->offsets.as<int64_t>();
+  a.num_docs = h->num_docs;
+  a.wave_docs = h->wave_docs.as<int64_t>();
+  a.num_waves = waves;
+  a.query_tokens = (int32_t)query_tokens;
+  a.scale = h->scale;
+  a.score_stride = h->num_docs;
+  a.counter = ticket_counter(h);
+  const int64_t per_pass = 128 / query_tokens;
+  for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
+    const int64_t nb = std::min(per_pass, batch - b0);
+    a.query = d_query + b0 * query_tokens * 128;
+    a.batch = (int32_t)nb;
+    a.scores = d_scores + b0 * h->num_docs;
+    a.k = fused_topk ? (int32_t)k : 0;
+    a.top_scores = fused_topk ? d_top_s + b0 * k : nullptr;
+    a.top_ids = fused_topk ? d_top_i + b0 * k : nullptr;
+    check_hip(launch_int8q_search(a, h->has_token_scale, stream), "launch int8q search kernel");
+  }
+  if (k > 0 && !fused_topk)
+    check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),
+              "launch int8q topk selection kernel");
+}
+
 void run_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                float* d_out, hipStream_t stream) {
-  quantize_int8q(h, d_query, batch, query_tokens, stream);
-  score_int8q(h, batch, query_tokens, d_out, stream);
+  search_int8q(h, d_query, batch, query_tokens, d_out, 0, nullptr, nullptr, stream);
 }
 
 float* ensure_scores(msim_int4_docs* h, int64_t batch, int64_t targets) {
@@ -254,6 +341,7 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
     h->scale = scale;
     h->packed_size = (uint64_t)num_tokens * (uint64_t)row_bytes;
     h->offsets_size = (uint64_t)num_offsets;
+    h->host_offsets.assign(offsets, offsets + num_offsets);
     h->packed.ensure(std::max<uint64_t>(h->packed_size, 64), "hipMalloc int4 packed docs");
     h->offsets.ensure(h->offsets_size * 8, "hipMalloc int4 offsets");
     if (h->packed_size)
@@ -371,10 +459,8 @@ extern "C" int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query,
     float* d_scores = ensure_scores(h, batch, h->num_docs);
     h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc int8q top score cache");
     h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc int8q top index cache");
-    run_int8q(h, d_query, batch, query_tokens, d_scores, stream);
-    check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr,
-                          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), stream),
-              "launch int8q topk selection kernel");
+    search_int8q(h, d_query, batch, query_tokens, d_scores, k, h->top_scores.as<float>(),
+                 h->top_indices.as<int64_t>(), stream);
     check_hip(hipMemcpyAsync(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top scores to host");
     check_hip(hipMemcpyAsync(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top indices to host");
     check_hip(hipStreamSynchronize(stream), "synchronize int8q topk kernels");
@@ -404,10 +490,7 @@ extern "C" int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_quer
     if (batch == 0) return;
     select_device(h->device);
     float* d_full = ensure_scores(h, batch, h->num_docs);
-    run_int8q(h, d_query, batch, query_tokens, d_full, as_stream(stream));
-    check_hip(launch_topk(d_full, batch, h->num_docs, h->num_docs, k, nullptr, d_scores, d_indices,
-                          as_stream(stream)),
-              "launch int8q topk selection kernel");
+    search_int8q(h, d_query, batch, query_tokens, d_full, k, d_scores, d_indices, as_stream(stream));
   });
 }
 

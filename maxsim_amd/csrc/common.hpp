@@ -33,6 +33,28 @@ __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Mark a 64-bit value as wave-uniform so it lives in SGPRs (it must already be
+// equal across the wave).
+__device__ __forceinline__ int64_t wave_uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Read-only view in the constant address space: uniform loads through it
+// become scalar loads (the data must not change during the kernel).
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* as_constant(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+
+// Order this wave's LDS accesses (no effect on global memory operations).
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(a, fmaxf(b, c)); }
 
 // numpy's pairwise float64 reduction order over a[0..n) for 8 < n <= 128 is

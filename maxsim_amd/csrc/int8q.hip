@@ -66,11 +66,7 @@ __global__ __launch_bounds__(256) void quantize_query_int8_kernel(
 // Per-wave scratch for the per-row maxima of one document.
 constexpr int kRowsPerPass = 128;
 
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+__device__ __forceinline__ void wave_lds_sync() { wave_sync_lds(); }
 
 // Finish one document: out[b] = f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale)
 // for the `batch` rows held in `rowmax` (query_tokens per batch row).

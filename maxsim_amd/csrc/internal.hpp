@@ -36,6 +36,33 @@ hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int
                                int64_t query_tokens, int64_t num_docs, double scale,
                                const int64_t* d_offsets, float* d_out, hipStream_t stream);
 
+// Arguments of the fused one-launch search (int8q_fused.hip): quantise, score
+// every document, and (k > 0) select the top-k of each batch row.
+constexpr int kFusedMaxK = 256;
+struct FusedArgs {
+  const uint8_t* codes;
+  const float* token_scale;   // nullptr for tensor-scale corpora
+  const int64_t* offsets;
+  int64_t num_docs;
+  const int64_t* wave_docs;   // [num_waves + 1] document range of each wave
+  int64_t num_waves;
+  const float* query;         // f32 [batch * query_tokens, 128] of this pass
+  int32_t batch;
+  int32_t query_tokens;
+  double scale;
+  float* scores;              // [batch, score_stride]
+  int64_t score_stride;
+  int32_t k;                  // 0: scores only
+  float* top_scores;          // [batch, k]
+  int64_t* top_ids;           // [batch, k]
+  uint32_t* counter;          // zero before the launch; the last workgroup resets it
+};
+hipError_t launch_int8q_search(const FusedArgs& args, bool token_scale, hipStream_t stream);
+// Waves per workgroup of the fused search kernel; the fused top-k tail needs
+// num_docs <= kFusedTailMaxDocs.
+int fused_waves_per_block();
+constexpr int64_t kFusedTailMaxDocs = 4096;
+
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a
 // position to the reported id.
