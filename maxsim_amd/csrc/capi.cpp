@@ -105,8 +105,9 @@ struct msim_int4_docs {
   bool has_residual = false;
   int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
   std::vector<int64_t> host_offsets;
-  int64_t partition_waves = 0;    // wave count the cached partition was built for
-  DeviceBuffer wave_docs, counter;
+  int64_t partition_waves = 0;    // wave count the cached scan table was built for
+  int64_t num_scan_waves = 0;     // rows of wave_info
+  DeviceBuffer wave_info, doc_table, ring_starts;
   DeviceBuffer packed, offsets, token_scales, residual_packed, residual_token_scales;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax, weights,
@@ -118,7 +119,7 @@ struct msim_int4_docs {
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap +
-           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_docs.cap + counter.cap;
+           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_info.cap + doc_table.cap + ring_starts.cap;
   }
 };
 
@@ -216,86 +217,70 @@ void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* 
   }
 }
 
-// Contiguous document ranges for `waves` waves, balanced by cost
-// ceil(len / 16) + 1 (16-token tiles plus the per-document finish).
-void build_partition(msim_int4_docs* h, int64_t waves) {
+// Scan tables of the handle for the requested wave count (cached).
+void build_wave_info(msim_int4_docs* h, int64_t waves) {
   if (h->partition_waves == waves) return;
-  const int64_t n = h->num_docs;
-  std::vector<int64_t> cost(n + 1, 0);
-  for (int64_t d = 0; d < n; ++d) {
-    const int64_t len = h->host_offsets[d + 1] - h->host_offsets[d];
-    cost[d + 1] = cost[d] + (len + 15) / 16 + 1;
-  }
-  std::vector<int64_t> part(waves + 1);
-  for (int64_t w = 0; w <= waves; ++w) {
-    const int64_t target = w == waves ? cost[n] + 1 : (cost[n] * w) / waves;
-    part[w] = std::lower_bound(cost.begin(), cost.end(), target) - cost.begin();
-    part[w] = std::min(part[w], n);
-  }
-  part[0] = 0;
-  part[waves] = n;
-  h->wave_docs.ensure(sizeof(int64_t) * (waves + 1), "hipMalloc wave partition");
-  check_hip(hipMemcpy(h->wave_docs.ptr, part.data(), sizeof(int64_t) * (waves + 1), hipMemcpyHostToDevice),
-            "copy wave partition to device");
+  std::vector<int64_t> info;
+  std::vector<uint64_t> table;
+  std::vector<uint32_t> ring;
+  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, table, ring);
+  h->num_scan_waves = (int64_t)info.size() / kWaveInfoWords;
+  h->wave_info.ensure(sizeof(int64_t) * info.size(), "hipMalloc scan wave table");
+  check_hip(hipMemcpy(h->wave_info.ptr, info.data(), sizeof(int64_t) * info.size(), hipMemcpyHostToDevice),
+            "copy scan wave table to device");
+  h->doc_table.ensure(sizeof(uint64_t) * std::max<size_t>(1, table.size()), "hipMalloc scan document table");
+  if (!table.empty())
+    check_hip(hipMemcpy(h->doc_table.ptr, table.data(), sizeof(uint64_t) * table.size(), hipMemcpyHostToDevice),
+              "copy scan document table to device");
+  h->ring_starts.ensure(sizeof(uint32_t) * std::max<size_t>(1, ring.size()), "hipMalloc scan ring table");
+  if (!ring.empty())
+    check_hip(hipMemcpy(h->ring_starts.ptr, ring.data(), sizeof(uint32_t) * ring.size(), hipMemcpyHostToDevice),
+              "copy scan ring table to device");
   h->partition_waves = waves;
 }
 
-int64_t search_waves(const msim_int4_docs* h) {
-  // Default: two resident workgroups of fused_waves_per_block() waves per CU.
+int64_t scan_waves(const msim_int4_docs* h) {
+  // Default: eight waves per CU (two per SIMD); a docs-per-wave override sets
+  // the count directly.
   int64_t waves = g_docs_per_wave > 0 ? (h->num_docs + g_docs_per_wave - 1) / g_docs_per_wave
-                                      : (int64_t)device_cu_count() * 2 * fused_waves_per_block();
-  waves = std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
-  return waves;
-}
-
-uint32_t* ticket_counter(msim_int4_docs* h) {
-  if (h->counter.cap == 0) {
-    h->counter.ensure(256, "hipMalloc top-k ticket");
-    check_hip(hipMemset(h->counter.ptr, 0, 256), "zero top-k ticket");
-  }
-  return h->counter.as<uint32_t>();
+                                      : (int64_t)device_cu_count() * 8;
+  return std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
 }
 
 // Full int8-query search: scores of every document into d_scores [B, N] and,
 // when k > 0, the top-k of each batch row into d_top_s / d_top_i [B, k].
+// Query quantisation, the scan (one launch per pass of <= 128 query rows) and
+// the selection are separate launches on one stream.
 void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                   float* d_scores, int64_t k, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   if (batch == 0) return;
-  const bool fused = query_tokens > 0 && query_tokens <= 128 && h->num_docs > 0;
-  if (!fused) {
-    quantize_int8q(h, d_query, batch, query_tokens, stream);
+  quantize_int8q(h, d_query, batch, query_tokens, stream);
+  if (query_tokens == 0 || h->num_docs == 0 || query_tokens > 128) {
     score_int8q(h, batch, query_tokens, d_scores, stream);
-    if (k > 0)
-      check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),
-                "launch int8q topk selection kernel");
-    return;
+  } else {
+    build_wave_info(h, scan_waves(h));
+    ScanArgs a{};
+    a.codes = h->packed.as<uint8_t>();
+    a.token_scale = h->has_token_scale ? h->token_scales.as<float>() : nullptr;
+    a.offsets = h->offsets.as<int64_t>();
+    a.wave_info = h->wave_info.as<int64_t>();
+    a.doc_table = h->doc_table.as<uint64_t>();
+    a.ring_starts = h->ring_starts.as<uint32_t>();
+    a.num_waves = h->num_scan_waves;
+    a.query_tokens = (int32_t)query_tokens;
+    a.scale = h->scale;
+    a.score_stride = h->num_docs;
+    const int64_t per_pass = 128 / query_tokens;
+    for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
+      const int64_t nb = std::min(per_pass, batch - b0);
+      a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;
+      a.qscale = h->qscale.as<float>() + b0 * query_tokens;
+      a.batch = (int32_t)nb;
+      a.scores = d_scores + b0 * h->num_docs;
+      check_hip(launch_int8q_scan(a, h->has_token_scale, stream), "launch int8q scan kernel");
+    }
   }
-  const int64_t waves = search_waves(h);
-  build_partition(h, waves);
-  const bool fused_topk = k > 0 && k <= kFusedMaxK && h->num_docs <= kFusedTailMaxDocs;
-  FusedArgs a{};
-  a.codes = h->packed.as<uint8_t>();
-  a.token_scale = h->has_token_scale ? h->token_scales.as<float>() : nullptr;
-  a.offsets = h->offsets.as<int64_t>();
-  a.num_docs = h->num_docs;
-  a.wave_docs = h->wave_docs.as<int64_t>();
-  a.num_waves = waves;
-  a.query_tokens = (int32_t)query_tokens;
-  a.scale = h->scale;
-  a.score_stride = h->num_docs;
-  a.counter = ticket_counter(h);
-  const int64_t per_pass = 128 / query_tokens;
-  for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
-    const int64_t nb = std::min(per_pass, batch - b0);
-    a.query = d_query + b0 * query_tokens * 128;
-    a.batch = (int32_t)nb;
-    a.scores = d_scores + b0 * h->num_docs;
-    a.k = fused_topk ? (int32_t)k : 0;
-    a.top_scores = fused_topk ? d_top_s + b0 * k : nullptr;
-    a.top_ids = fused_topk ? d_top_i + b0 * k : nullptr;
-    check_hip(launch_int8q_search(a, h->has_token_scale, stream), "launch int8q search kernel");
-  }
-  if (k > 0 && !fused_topk)
+  if (k > 0)
     check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),
               "launch int8q topk selection kernel");
 }

@@ -25,8 +25,68 @@ __device__ __forceinline__ v4u load_b128(__amdgpu_buffer_rsrc_t r, int byte_offs
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0);
 }
 
+__device__ __forceinline__ uint64_t load_b64(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_offset, 0, 0);
+  return ((uint64_t)v.y << 32) | v.x;
+}
+
 __device__ __forceinline__ unsigned load_b32(__amdgpu_buffer_rsrc_t r, int byte_offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 0);
+}
+
+// Buffer descriptor as an SGPR quad (for the inline-assembly loads below).
+__device__ __forceinline__ v4i make_rsrc_words(const void* base, uint32_t num_bytes) {
+  const uint64_t a = (uint64_t)base;
+  return (v4i){(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xFFFF, (int)num_bytes, kBufferFlags};
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Buffer loads whose destination is LDS: lane l writes its 16 (4) bytes at
+// LDS address lds + 16 l (4 l), lds being wave-uniform.  They are issued from
+// inline assembly so that the compiler's conservative LDS-DMA tracking does
+// not add a full vmcnt wait before every later LDS read; in exchange, the
+// code must wait with vm_wait_lds<N>() (N = vector memory instructions
+// issued after the load that may still be in flight) before reading the
+// data.  M0 carries the LDS base (an SALU write of M0 needs one wait state
+// before a load with the LDS destination reads it) and is restored afterwards.
+__device__ __forceinline__ void lds_load_b128(v4i rsrc, uint32_t byte_offset, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_nop 1\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(byte_offset), "s"(rsrc)
+      : "memory");
+}
+__device__ __forceinline__ void lds_load_b32(v4i rsrc, uint32_t byte_offset, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %2, %3, 0 offen lds\n\ts_nop 1\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(byte_offset), "s"(rsrc)
+      : "memory");
+}
+
+// A use of `v` at this point: the compiler completes its load here.
+template <typename T>
+__device__ __forceinline__ void use_here(const T& v) {
+  asm volatile("" ::"v"(v));
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait_lds() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Orders a later LDS-destination load into the slot these registers were
+// read from after the read itself (the registers must hold the data first).
+// Never issue loads with a register destination outside compiler tracking:
+// the register allocator may copy such a register before the data lands.
+__device__ __forceinline__ void lds_read_done(const v4u& w, uint32_t s) {
+  asm volatile("" ::"v"(w), "v"(s) : "memory");
 }
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
@@ -53,6 +113,12 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Value of lane 4 * (l / 4) + I in every lane l (DPP quad permute).
+template <int I>
+__device__ __forceinline__ uint32_t quad_broadcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, I * 0x55, 0xF, 0xF, false);
 }
 
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(a, fmaxf(b, c)); }

@@ -1,0 +1,391 @@
+// int8q_scan.hip -- int4 documents x int8-quantised queries: full-corpus scan
+// on gfx950 MFMA.
+//
+// Semantics restated from the reference: token-scaled MaxSim cu:1569-1627 /
+// tests/test_int4_int8q.py:15-26 (scale before max, empty doc -> 0), with the
+// query rows already quantised by quantize_query_int8_kernel (int8q.hip).
+// Scores equal the C oracle bit for bit.
+//
+// Work split: every wave owns a contiguous range of documents (balanced by
+// 16-token tiles on the host, see ScanArgs) and walks its non-empty
+// documents as one stream of 16-token tiles.  The four waves of a workgroup
+// are independent (no barriers).
+//  * a document of len >= 16 tokens is covered by ceil(len / 16) tiles whose
+//    last one is shifted back to end at the document end (it re-reads up to
+//    15 tokens: max is idempotent), so every tile has 16 valid rows; only
+//    documents shorter than 16 tokens need row masking;
+//  * kPrefetch tiles of codes and token scales are in flight per wave,
+//    loaded global -> LDS into a per-wave ring and read back one tile ahead
+//    of use; every global load is issued without compiler tracking and
+//    waited for explicitly (common.hpp), so the steady state has exactly one
+//    vmcnt wait per tile;
+//  * the query tiles (B operands, <= 128 rows) live in registers for the
+//    life of the wave; v_mfma_i32_16x16x64_i8 forms exact dots with each code
+//    byte's nibbles masked in place as int8 (hi = w & 0xF0, lo = (w << 4) &
+//    0xF0), i.e. sixteen times the signed value, so acc = 16 * dot and
+//    float(acc) * (s_t / 16) rounds the same real number as float(dot) * s_t;
+//  * software pipelined: the MFMAs of tile i are issued before the VALU
+//    epilogue (scale, running max) of tile i - 1;
+//  * at a document end: cross-lane max with permlane swaps and numpy's
+//    float64 pairwise sum over query tokens.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace msim {
+
+constexpr int kScanThreads = 256;
+constexpr int kScanWaves = kScanThreads / kWave;
+constexpr int kPrefetch = kScanPrefetch;  // tiles in flight per wave
+static_assert(kPrefetch >= 2, "ring of at least two tiles");
+
+// Maximum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
+__device__ __forceinline__ float max_over_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// out[b * stride] = f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale), b < batch.
+// rows = batch * query_tokens <= 128, so query_tokens < 8 means batch <= 128
+// (lanes b and b + 64) and query_tokens >= 8 means batch <= 16 (two rounds of
+// eight lanes per batch row).  Each path issues at most two global stores.
+static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, const float* qs, int batch,
+                                                       int query_tokens, double scale,
+                                                       float* __restrict__ out, int64_t stride) {
+  const int lane = lane_id();
+  auto prod = [&](int r) -> double { return (double)rowmax[r] * (double)qs[r]; };
+  if (query_tokens < 8) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int b = lane + kWave * h;
+      double res = 0.0;
+      if (b < batch) {
+        for (int q = 0; q < query_tokens; ++q) res = __dadd_rn(res, prod(b * query_tokens + q));
+        out[(int64_t)b * stride] = (float)(res * scale);
+      }
+    }
+    return;
+  }
+  const int body = query_tokens - (query_tokens % 8);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (8 * h >= batch) break;
+    const int b = 8 * h + (lane >> 3), k = lane & 7;
+    const bool valid = b < batch;
+    const int base = valid ? b * query_tokens : 0;
+    double r = prod(base + k);
+    for (int i = 8 + k; i < body; i += 8) r = __dadd_rn(r, prod(base + i));
+    double o = __shfl_xor(r, 1);
+    if ((k & 1) == 0) r = __dadd_rn(r, o);
+    o = __shfl_xor(r, 2);
+    if ((k & 3) == 0) r = __dadd_rn(r, o);
+    o = __shfl_xor(r, 4);
+    if (k == 0) r = __dadd_rn(r, o);
+    if (k == 0 && valid) {
+      for (int i = body; i < query_tokens; ++i) r = __dadd_rn(r, prod(base + i));
+      out[(int64_t)b * stride] = (float)(r * scale);
+    }
+  }
+}
+
+template <int NT, bool kTS>
+__global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
+    ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale,
+    const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
+    const uint64_t* __restrict__ doc_table, const int8_t* __restrict__ qpack,
+    const float* __restrict__ qscale, float* __restrict__ scores) {
+  // Per wave: the tile ring (codes as 64 lanes x 16 B, token scales as 64
+  // lanes x 4 B per slot), the per-row maxima of the document being finished
+  // and the query scales.
+  __shared__ __attribute__((aligned(16))) v4u s_codes[kScanWaves][kPrefetch][kWave];
+  __shared__ uint32_t s_scales[kScanWaves][kPrefetch][kWave];
+  __shared__ float s_rowmax[kScanWaves][128];
+  __shared__ float s_qscale[kScanWaves][128];
+  const int lane = lane_id();
+  const int wave = wave_uniform(threadIdx.x / kWave);
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t gw = (int64_t)blockIdx.x * kScanWaves + wave;
+  if (gw >= p.num_waves) return;
+
+  const auto info = as_constant(wave_info_ptr) + gw * kWaveInfoWords;
+  const int64_t d0 = info[0];
+  const int ndocs = (int)info[1];
+  const int64_t T0 = info[2], T1 = info[3];
+  const int ntiles = (int)info[4];
+  const int n_ne = (int)info[5];
+  const int64_t tab0 = info[6];
+  const uint32_t first_end = (uint32_t)info[7];
+  const bool has_empty = (info[7] >> 32) != 0;
+  float* rowmax = s_rowmax[wave];
+  float* qs = s_qscale[wave];
+
+  // Loads, in this order: the document table and offsets (compiler-tracked),
+  // the query scales and the first kPrefetch ring tiles (LDS destination,
+  // untracked), the query tiles (compiler-tracked).  All of them complete
+  // before the first step.
+  //
+  // Document table: lane k holds (end of the k-th non-empty document relative
+  // to T0, its local index) for k < n_ne.
+  // (Bounds-checked loads: lanes past the end read zero without a branch.)
+  const uint64_t dtab = load_b64(make_rsrc(doc_table + tab0, (uint32_t)(n_ne * 8)), 8 * lane);
+  auto doc_end = [&](int k) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)dtab, k); };
+  auto doc_local = [&](int k) -> int { return __builtin_amdgcn_readlane((int)(uint32_t)(dtab >> 32), k); };
+  // Document offsets (lane i: offsets[d0 + i], i <= ndocs), only when the
+  // wave has empty documents.
+  const uint64_t offv =
+      load_b64(make_rsrc(offsets + d0, has_empty ? (uint32_t)((ndocs + 1) * 8) : 0u), 8 * lane);
+
+  // Query scales to LDS for the document finish (rows past 16 * NT read zero).
+  {
+    const v4i rq = make_rsrc_words(qscale, (uint32_t)(16 * NT * 4));
+    const uint32_t q_lds = wave_uniform((int)lds_address(qs));
+    lds_load_b32(rq, 4u * (uint32_t)lane, q_lds);
+    lds_load_b32(rq, 4u * (uint32_t)(lane + kWave), q_lds + 4 * kWave);
+  }
+
+  // Bounds-checked descriptors over the wave's tokens (rows past the wave
+  // read zero).
+  const v4i rc = make_rsrc_words(codes + T0 * 64, (uint32_t)((T1 - T0) * 64));
+  const v4i rs = make_rsrc_words(kTS ? (const void*)(token_scale + T0) : (const void*)codes,
+                                 kTS ? (uint32_t)((T1 - T0) * 4) : 0u);
+  const uint32_t ring_codes = wave_uniform((int)lds_address(&s_codes[wave][0][0]));
+  const uint32_t ring_scales = wave_uniform((int)lds_address(&s_scales[wave][0][0]));
+
+  // Tiles of document [s, e) (token offsets relative to T0) start at s,
+  // s + 16, ..., with the last one at max(s, e - 16).  Lane (g, c) fetches
+  // the 16 code bytes of token t + c for dims [32g, 32g + 32) and the scale
+  // of token t + 4g + (c & 3); the four scales a lane needs (its accumulator
+  // rows 4g..4g+3) are then quad broadcasts.  Every step issues exactly
+  // kOps loads, so slot i is complete once vmcnt <= (kPrefetch - 1) * kOps.
+  constexpr int kOps = kTS ? 2 : 1;
+  constexpr int kRingWait = (kPrefetch - 1) * kOps;
+  const uint32_t sc_lane = 4u * (uint32_t)g + ((uint32_t)c & 3u);
+  auto load_tile = [&](int slot_, uint32_t t) {
+    lds_load_b128(rc, (t + (uint32_t)c) * 64u + 16u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
+    if (kTS) lds_load_b32(rs, (t + sc_lane) * 4u, ring_scales + slot_ * kWave * 4);
+  };
+  // The first kPrefetch tile starts and the load cursor after them come from
+  // the host (the cursor needs the document table only from then on).
+  const auto ring0 = as_constant(p.ring_starts) + gw * kScanRingWords;
+#pragma unroll
+  for (int s = 0; s < kPrefetch; ++s) load_tile(s, ring0[s]);
+  int ld_k = (int)ring0[kPrefetch];
+  uint32_t ld_t = ring0[kPrefetch + 1], ld_e = ring0[kPrefetch + 2];
+  auto issue = [&](int slot_) {
+    load_tile(slot_, ld_t);
+    if (ld_t != kScanPastEnd) {
+      const uint32_t nt = ld_t + 16u;
+      if (nt >= ld_e) {
+        ++ld_k;
+        if (ld_k < n_ne) {
+          ld_t = ld_e;
+          ld_e = doc_end(ld_k);
+        } else {
+          ld_t = kScanPastEnd;
+        }
+      } else {
+        ld_t = nt + 16u <= ld_e ? nt : ld_e - 16u;
+      }
+    }
+  };
+
+  // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g.
+  v4i blo[NT], bhi[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const v4i* src = reinterpret_cast<const v4i*>(qpack + (int64_t)(16 * j + c) * 128 + 32 * g);
+    blo[j] = src[0];
+    bhi[j] = src[1];
+  }
+  // Complete every load issued so far (the compiler's waits for its own
+  // loads here also cover the older LDS-destination ones).
+  use_here(dtab);
+  use_here(offv);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    use_here(blo[j]);
+    use_here(bhi[j]);
+  }
+  vm_wait_lds<0>();
+
+  // Current tile, read back from the ring one step ahead of its use.
+  vm_wait_lds<kRingWait>();
+  v4u w = s_codes[wave][0][lane];
+  uint32_t sv = kTS ? s_scales[wave][0][lane] : 0u;
+
+  // Compute cursor: the tile whose MFMAs are issued in this step ...
+  int cp_k = 0;
+  uint32_t cp_t = 0u, cp_e = first_end;
+  // ... and the document of the tile whose epilogue runs in this step.
+  int pv_k = 0;
+  bool pv_last = false;
+
+  float m[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) m[j] = kNegInf;
+  v4i acc[2][NT];
+  float sc[2][4];
+  constexpr float kInf = __builtin_huge_valf();
+
+  // Epilogue of the tile in acc[par] / sc[par]: running max per query row.
+  // A masked row has acc = -2^30 + 16 * dot < 0 and scale +inf, i.e. -inf.
+  auto epilogue_max = [&](int par) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const float x0 = (float)acc[par][j][0] * sc[par][0];
+      const float x1 = (float)acc[par][j][1] * sc[par][1];
+      const float x2 = (float)acc[par][j][2] * sc[par][2];
+      const float x3 = (float)acc[par][j][3] * sc[par][3];
+      m[j] = fmaxf(fmaxf(fmaxf(m[j], x0), x1), fmaxf(x2, x3));
+    }
+  };
+  // Document end: per-row maxima over the four lane groups, then the score.
+  auto finish = [&](int k) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) m[j] = max_over_groups(m[j]);
+    if (g == 0) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = m[j];
+    }
+    wave_sync_lds();
+    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + doc_local(k), p.score_stride);
+    wave_sync_lds();
+#pragma unroll
+    for (int j = 0; j < NT; ++j) m[j] = kNegInf;
+  };
+
+  // One pipeline step for the tile in `w` (ring slot `slot`): refill of that
+  // slot, read-back of the next tile, then the tile's MFMAs interleaved with
+  // the epilogue of the previous tile (accumulator set par ^ 1).  Only two
+  // copies of the step are unrolled (the ring slot is a runtime value) to keep
+  // the loop within the instruction cache.
+  int slot = 0;
+  auto step = [&](int par, bool has_prev) {
+    v4i lo, hi;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      hi[x] = (int)(w[x] & 0xF0F0F0F0u);
+      lo[x] = (int)((w[x] << 4) & 0xF0F0F0F0u);
+    }
+    float s0 = 0.0625f, s1 = 0.0625f, s2 = 0.0625f, s3 = 0.0625f;
+    if (kTS) {
+      s0 = __uint_as_float(quad_broadcast<0>(sv)) * 0.0625f;
+      s1 = __uint_as_float(quad_broadcast<1>(sv)) * 0.0625f;
+      s2 = __uint_as_float(quad_broadcast<2>(sv)) * 0.0625f;
+      s3 = __uint_as_float(quad_broadcast<3>(sv)) * 0.0625f;
+    }
+    // Rows of this tile past a short document are masked: their accumulators
+    // start at -2^30 (|16 * dot| < 2^22) and their scales are +inf.
+    const uint32_t rows = cp_e - cp_t < 16u ? cp_e - cp_t : 16u;
+    v4i cinit = (v4i){0, 0, 0, 0};
+    if (rows < 16u) {
+      const uint32_t r0 = 4u * (uint32_t)g;
+      constexpr int kLow = -(1 << 30);
+      cinit = (v4i){r0 + 0u < rows ? 0 : kLow, r0 + 1u < rows ? 0 : kLow, r0 + 2u < rows ? 0 : kLow,
+                    r0 + 3u < rows ? 0 : kLow};
+      s0 = r0 + 0u < rows ? s0 : kInf;
+      s1 = r0 + 1u < rows ? s1 : kInf;
+      s2 = r0 + 2u < rows ? s2 : kInf;
+      s3 = r0 + 3u < rows ? s3 : kInf;
+    }
+    sc[par][0] = s0;
+    sc[par][1] = s1;
+    sc[par][2] = s2;
+    sc[par][3] = s3;
+    // The slot's contents are in registers before the refill may land.
+    lds_read_done(w, sv);
+    issue(slot);
+    // Next tile: wait for its slot and read it back (consumed next step).
+    slot = slot + 1 == kPrefetch ? 0 : slot + 1;
+    vm_wait_lds<kRingWait>();
+    w = s_codes[wave][slot][lane];
+    if (kTS) sv = s_scales[wave][slot][lane];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+      acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc[par][j], 0, 0, 0);
+    }
+    if (has_prev) {
+      epilogue_max(par ^ 1);
+      // One MFMA, then five VALU instructions of the previous tile's epilogue.
+#pragma unroll
+      for (int j = 0; j < 2 * NT; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      }
+      if (pv_last) finish(pv_k);
+    }
+    // Advance the compute cursor past this tile.
+    const bool last = cp_t + 16u >= cp_e;
+    pv_k = cp_k;
+    pv_last = last;
+    if (last) {
+      ++cp_k;
+      cp_t = cp_e;
+      cp_e = cp_k < n_ne ? doc_end(cp_k) : cp_e;
+    } else {
+      cp_t = cp_t + 32u <= cp_e ? cp_t + 16u : cp_e - 16u;
+    }
+  };
+
+  if (ntiles > 0) {
+    // Tile i lives in ring slot i % kPrefetch and accumulator set i & 1.
+    step(0, false);
+    int i = 1;
+    for (; i + 2 <= ntiles; i += 2) {
+      step(1, true);
+      step(0, true);
+    }
+    if (i < ntiles) {
+      step(1, true);
+      epilogue_max(1);
+    } else {
+      epilogue_max(0);
+    }
+    finish(pv_k);  // the last tile always ends a document
+  }
+  // No LDS-destination load may still be in flight when the wave ends.
+  vm_wait_lds<0>();
+
+  // Empty documents score 0 (lane d owns local document d).
+  if (has_empty) {
+    const uint64_t next = ((uint64_t)(uint32_t)__shfl_down((int)(uint32_t)(offv >> 32), 1) << 32) |
+                          (uint32_t)__shfl_down((int)(uint32_t)offv, 1);
+    if (lane < ndocs && next == offv) {
+      for (int b = 0; b < p.batch; ++b) scores[(int64_t)b * p.score_stride + d0 + lane] = 0.0f;
+    }
+  }
+}
+
+template <bool kTS>
+static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_t stream) {
+  const dim3 grid((unsigned)blocks), block(kScanThreads);
+  switch (nt) {
+#define MSIM_SCAN_CASE(N)                                                                           \
+  int8q_scan_kernel<N, kTS><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale, a.offsets,        \
+                                                        a.wave_info, a.doc_table, a.qpack, a.qscale, \
+                                                        a.scores)
+    case 1: MSIM_SCAN_CASE(1); break;
+    case 2: MSIM_SCAN_CASE(2); break;
+    case 3: MSIM_SCAN_CASE(3); break;
+    case 4: MSIM_SCAN_CASE(4); break;
+    case 5: MSIM_SCAN_CASE(5); break;
+    case 6: MSIM_SCAN_CASE(6); break;
+    case 7: MSIM_SCAN_CASE(7); break;
+    default: MSIM_SCAN_CASE(8); break;
+#undef MSIM_SCAN_CASE
+  }
+}
+
+hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream) {
+  const int rows = args.batch * args.query_tokens;
+  if (rows <= 0 || rows > 128 || args.num_waves <= 0) return hipErrorInvalidValue;
+  const int nt = (rows + 15) / 16;
+  const int64_t blocks = (args.num_waves + kScanWaves - 1) / kScanWaves;
+  if (token_scale) launch_scan_nt<true>(args, nt, blocks, stream);
+  else launch_scan_nt<false>(args, nt, blocks, stream);
+  return hipGetLastError();
+}
+
+}  // namespace msim
