@@ -107,19 +107,19 @@ struct msim_int4_docs {
   std::vector<int64_t> host_offsets;
   int64_t partition_waves = 0;    // wave count the cached scan table was built for
   int64_t num_scan_waves = 0;     // rows of wave_info
-  DeviceBuffer wave_info, doc_table, ring_starts;
-  DeviceBuffer packed, offsets, token_scales, residual_packed, residual_token_scales;
+  DeviceBuffer wave_info, tile_table;
+  DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax, weights,
       candidates;
 
   uint64_t resident_bytes() const {
-    return packed_size + offsets_size * 8 + token_scales.cap + residual_packed.cap +
+    return packed_size + offsets_size * 8 + token_scales.cap + token_scales16.cap + residual_packed.cap +
            residual_token_scales.cap;
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap +
-           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_info.cap + doc_table.cap + ring_starts.cap;
+           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_info.cap + tile_table.cap;
   }
 };
 
@@ -146,8 +146,9 @@ void quantize_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int6
   const int64_t rows = batch * query_tokens;
   h->quantized_rows = -1;
   if (rows == 0) return;
-  // Passes read up to 15 rows past their last valid row; pad so they stay in bounds.
-  const int64_t rows_padded = ((rows + 15) / 16) * 16 + 16;
+  // Kernels read whole 16-row query tiles, up to 128 rows from a pass's
+  // first row; pad (with zero rows) so those reads stay in bounds.
+  const int64_t rows_padded = ((rows + 15) / 16) * 16 + 128;
   h->qpack.ensure(rows_padded * 128, "hipMalloc int8q query codes");
   h->qscale.ensure(rows_padded * 4, "hipMalloc int8q query scales");
   h->qbias.ensure(rows_padded * 4, "hipMalloc int8q query bias");
@@ -221,21 +222,17 @@ void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* 
 void build_wave_info(msim_int4_docs* h, int64_t waves) {
   if (h->partition_waves == waves) return;
   std::vector<int64_t> info;
-  std::vector<uint64_t> table;
-  std::vector<uint32_t> ring;
-  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, table, ring);
+  std::vector<uint64_t> tiles;
+  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, tiles);
   h->num_scan_waves = (int64_t)info.size() / kWaveInfoWords;
-  h->wave_info.ensure(sizeof(int64_t) * info.size(), "hipMalloc scan wave table");
-  check_hip(hipMemcpy(h->wave_info.ptr, info.data(), sizeof(int64_t) * info.size(), hipMemcpyHostToDevice),
-            "copy scan wave table to device");
-  h->doc_table.ensure(sizeof(uint64_t) * std::max<size_t>(1, table.size()), "hipMalloc scan document table");
-  if (!table.empty())
-    check_hip(hipMemcpy(h->doc_table.ptr, table.data(), sizeof(uint64_t) * table.size(), hipMemcpyHostToDevice),
-              "copy scan document table to device");
-  h->ring_starts.ensure(sizeof(uint32_t) * std::max<size_t>(1, ring.size()), "hipMalloc scan ring table");
-  if (!ring.empty())
-    check_hip(hipMemcpy(h->ring_starts.ptr, ring.data(), sizeof(uint32_t) * ring.size(), hipMemcpyHostToDevice),
-              "copy scan ring table to device");
+  h->wave_info.ensure(sizeof(int64_t) * std::max<size_t>(1, info.size()), "hipMalloc scan wave table");
+  if (!info.empty())
+    check_hip(hipMemcpy(h->wave_info.ptr, info.data(), sizeof(int64_t) * info.size(), hipMemcpyHostToDevice),
+              "copy scan wave table to device");
+  h->tile_table.ensure(sizeof(uint64_t) * std::max<size_t>(1, tiles.size()), "hipMalloc scan tile table");
+  if (!tiles.empty())
+    check_hip(hipMemcpy(h->tile_table.ptr, tiles.data(), sizeof(uint64_t) * tiles.size(), hipMemcpyHostToDevice),
+              "copy scan tile table to device");
   h->partition_waves = waves;
 }
 
@@ -261,11 +258,10 @@ void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_
     build_wave_info(h, scan_waves(h));
     ScanArgs a{};
     a.codes = h->packed.as<uint8_t>();
-    a.token_scale = h->has_token_scale ? h->token_scales.as<float>() : nullptr;
+    a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
     a.offsets = h->offsets.as<int64_t>();
     a.wave_info = h->wave_info.as<int64_t>();
-    a.doc_table = h->doc_table.as<uint64_t>();
-    a.ring_starts = h->ring_starts.as<uint32_t>();
+    a.tile_table = h->tile_table.as<uint64_t>();
     a.num_waves = h->num_scan_waves;
     a.query_tokens = (int32_t)query_tokens;
     a.scale = h->scale;
@@ -353,6 +349,14 @@ extern "C" int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_s
     h->token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector");
     if (count)
       check_hip(hipMemcpy(h->token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 token scale vector to device");
+    // The int8-query scan multiplies 16 * dot by s / 16 (a power-of-two
+    // rescale, exact for normal floats).
+    std::vector<float> scaled(token_scales, token_scales + count);
+    for (float& v : scaled) v *= 0.0625f;
+    h->token_scales16.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector / 16");
+    if (count)
+      check_hip(hipMemcpy(h->token_scales16.ptr, scaled.data(), count * 4, hipMemcpyHostToDevice),
+                "copy int4 token scale vector / 16 to device");
     h->has_token_scale = true;
   });
 }

@@ -57,7 +57,7 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 __device__ __forceinline__ void lds_load_b128(v4i rsrc, uint32_t byte_offset, uint32_t lds) {
   uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_nop 1\n\ts_mov_b32 m0, %0"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
       : "=&s"(saved)
       : "s"(lds), "v"(byte_offset), "s"(rsrc)
       : "memory");
@@ -65,7 +65,7 @@ __device__ __forceinline__ void lds_load_b128(v4i rsrc, uint32_t byte_offset, ui
 __device__ __forceinline__ void lds_load_b32(v4i rsrc, uint32_t byte_offset, uint32_t lds) {
   uint32_t saved;
   asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %2, %3, 0 offen lds\n\ts_nop 1\n\ts_mov_b32 m0, %0"
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
       : "=&s"(saved)
       : "s"(lds), "v"(byte_offset), "s"(rsrc)
       : "memory");
@@ -85,8 +85,9 @@ __device__ __forceinline__ void vm_wait_lds() {
 // read from after the read itself (the registers must hold the data first).
 // Never issue loads with a register destination outside compiler tracking:
 // the register allocator may copy such a register before the data lands.
-__device__ __forceinline__ void lds_read_done(const v4u& w, uint32_t s) {
-  asm volatile("" ::"v"(w), "v"(s) : "memory");
+template <typename A, typename B>
+__device__ __forceinline__ void lds_read_done(const A& a, const B& b) {
+  asm volatile("" ::"v"(a), "v"(b) : "memory");
 }
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }

@@ -91,135 +91,94 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
 
 template <int NT, bool kTS>
 __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
-    ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale,
+    ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale16,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
-    const uint64_t* __restrict__ doc_table, const int8_t* __restrict__ qpack,
+    const uint64_t* __restrict__ tile_table, const int8_t* __restrict__ qpack,
     const float* __restrict__ qscale, float* __restrict__ scores) {
-  // Per wave: the tile ring (codes as 64 lanes x 16 B, token scales as 64
-  // lanes x 4 B per slot), the per-row maxima of the document being finished
-  // and the query scales.
+  // LDS: the workgroup's copy of the query tiles; per wave the tile ring
+  // (codes as 64 lanes x 16 B, token scales as 64 lanes x 4 B per slot), the
+  // per-row maxima of the document being finished and the query scales.
+  constexpr int kQueryParts = (NT + 1) / 2;  // 16-byte loads per lane for the query tiles
+  __shared__ __attribute__((aligned(16))) v4u s_query[kQueryParts * kScanWaves * kWave];
   __shared__ __attribute__((aligned(16))) v4u s_codes[kScanWaves][kPrefetch][kWave];
-  __shared__ uint32_t s_scales[kScanWaves][kPrefetch][kWave];
+  __shared__ __attribute__((aligned(16))) uint32_t s_scales[kScanWaves][kPrefetch][kWave];
   __shared__ float s_rowmax[kScanWaves][128];
   __shared__ float s_qscale[kScanWaves][128];
   const int lane = lane_id();
   const int wave = wave_uniform(threadIdx.x / kWave);
   const int g = lane >> 4, c = lane & 15;
+  // The host pads the wave table to whole workgroups (padding waves have no
+  // tiles), so every wave reaches the barrier below.
   const int64_t gw = (int64_t)blockIdx.x * kScanWaves + wave;
-  if (gw >= p.num_waves) return;
 
   const auto info = as_constant(wave_info_ptr) + gw * kWaveInfoWords;
   const int64_t d0 = info[0];
   const int ndocs = (int)info[1];
   const int64_t T0 = info[2], T1 = info[3];
   const int ntiles = (int)info[4];
-  const int n_ne = (int)info[5];
-  const int64_t tab0 = info[6];
-  const uint32_t first_end = (uint32_t)info[7];
-  const bool has_empty = (info[7] >> 32) != 0;
+  const auto tt = as_constant(tile_table) + info[5];
+  const bool has_empty = info[6] != 0;
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
 
-  // Loads, in this order: the document table and offsets (compiler-tracked),
-  // the query scales and the first kPrefetch ring tiles (LDS destination,
-  // untracked), the query tiles (compiler-tracked).  All of them complete
-  // before the first step.
-  //
-  // Document table: lane k holds (end of the k-th non-empty document relative
-  // to T0, its local index) for k < n_ne.
-  // (Bounds-checked loads: lanes past the end read zero without a branch.)
-  const uint64_t dtab = load_b64(make_rsrc(doc_table + tab0, (uint32_t)(n_ne * 8)), 8 * lane);
-  auto doc_end = [&](int k) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)dtab, k); };
-  auto doc_local = [&](int k) -> int { return __builtin_amdgcn_readlane((int)(uint32_t)(dtab >> 32), k); };
-  // Document offsets (lane i: offsets[d0 + i], i <= ndocs), only when the
-  // wave has empty documents.
-  const uint64_t offv =
-      load_b64(make_rsrc(offsets + d0, has_empty ? (uint32_t)((ndocs + 1) * 8) : 0u), 8 * lane);
-
-  // Query scales to LDS for the document finish (rows past 16 * NT read zero).
+  // Global loads, all with an LDS destination (untracked by the compiler,
+  // waited for explicitly), in this order: the workgroup's query tiles (each
+  // wave a quarter), this wave's query scales, the first kPrefetch tiles.
   {
+    const v4i rqp = make_rsrc_words(qpack, (uint32_t)(NT * 16 * 128));
+    const uint32_t q_lds = wave_uniform((int)lds_address(s_query));
+#pragma unroll
+    for (int i = 0; i < kQueryParts; ++i) {
+      const uint32_t part = (uint32_t)((i * kScanWaves + wave) * kWave);
+      lds_load_b128(rqp, (part + (uint32_t)lane) * 16u, q_lds + part * 16u);
+    }
     const v4i rq = make_rsrc_words(qscale, (uint32_t)(16 * NT * 4));
-    const uint32_t q_lds = wave_uniform((int)lds_address(qs));
-    lds_load_b32(rq, 4u * (uint32_t)lane, q_lds);
-    lds_load_b32(rq, 4u * (uint32_t)(lane + kWave), q_lds + 4 * kWave);
+    const uint32_t qs_lds = wave_uniform((int)lds_address(qs));
+    lds_load_b32(rq, 4u * (uint32_t)lane, qs_lds);
+    lds_load_b32(rq, 4u * (uint32_t)(lane + kWave), qs_lds + 4 * kWave);
   }
 
   // Bounds-checked descriptors over the wave's tokens (rows past the wave
   // read zero).
   const v4i rc = make_rsrc_words(codes + T0 * 64, (uint32_t)((T1 - T0) * 64));
-  const v4i rs = make_rsrc_words(kTS ? (const void*)(token_scale + T0) : (const void*)codes,
+  const v4i rs = make_rsrc_words(kTS ? (const void*)(token_scale16 + T0) : (const void*)codes,
                                  kTS ? (uint32_t)((T1 - T0) * 4) : 0u);
   const uint32_t ring_codes = wave_uniform((int)lds_address(&s_codes[wave][0][0]));
   const uint32_t ring_scales = wave_uniform((int)lds_address(&s_scales[wave][0][0]));
 
-  // Tiles of document [s, e) (token offsets relative to T0) start at s,
-  // s + 16, ..., with the last one at max(s, e - 16).  Lane (g, c) fetches
-  // the 16 code bytes of token t + c for dims [32g, 32g + 32) and the scale
-  // of token t + 4g + (c & 3); the four scales a lane needs (its accumulator
-  // rows 4g..4g+3) are then quad broadcasts.  Every step issues exactly
-  // kOps loads, so slot i is complete once vmcnt <= (kPrefetch - 1) * kOps.
+  // Tile i of the wave starts at token tt[i] (low 32 bits, relative to T0):
+  // documents of len >= 16 are covered by tiles at s, s + 16, ..., with the
+  // last one at e - 16.  Lane (g, c) fetches the 16 code bytes of token
+  // t + c for dims [32g, 32g + 32) and the (pre-divided by 16) scale of
+  // token t + c; a lane then reads the four scales of its accumulator rows
+  // 4g..4g+3 as one 16-byte LDS read.  Every step issues exactly kOps loads,
+  // so slot i is complete once vmcnt <= (kPrefetch - 1) * kOps.
   constexpr int kOps = kTS ? 2 : 1;
   constexpr int kRingWait = (kPrefetch - 1) * kOps;
-  const uint32_t sc_lane = 4u * (uint32_t)g + ((uint32_t)c & 3u);
   auto load_tile = [&](int slot_, uint32_t t) {
     lds_load_b128(rc, (t + (uint32_t)c) * 64u + 16u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
-    if (kTS) lds_load_b32(rs, (t + sc_lane) * 4u, ring_scales + slot_ * kWave * 4);
+    if (kTS) lds_load_b32(rs, (t + (uint32_t)c) * 4u, ring_scales + slot_ * kWave * 4);
   };
-  // The first kPrefetch tile starts and the load cursor after them come from
-  // the host (the cursor needs the document table only from then on).
-  const auto ring0 = as_constant(p.ring_starts) + gw * kScanRingWords;
 #pragma unroll
-  for (int s = 0; s < kPrefetch; ++s) load_tile(s, ring0[s]);
-  int ld_k = (int)ring0[kPrefetch];
-  uint32_t ld_t = ring0[kPrefetch + 1], ld_e = ring0[kPrefetch + 2];
-  auto issue = [&](int slot_) {
-    load_tile(slot_, ld_t);
-    if (ld_t != kScanPastEnd) {
-      const uint32_t nt = ld_t + 16u;
-      if (nt >= ld_e) {
-        ++ld_k;
-        if (ld_k < n_ne) {
-          ld_t = ld_e;
-          ld_e = doc_end(ld_k);
-        } else {
-          ld_t = kScanPastEnd;
-        }
-      } else {
-        ld_t = nt + 16u <= ld_e ? nt : ld_e - 16u;
-      }
-    }
-  };
+  for (int s = 0; s < kPrefetch; ++s) load_tile(s, (uint32_t)tt[s]);
 
+  // The query tiles (and scales) are complete once at most kPrefetch * kOps
+  // loads are outstanding; the barrier publishes all four quarters.
+  vm_wait_lds<kPrefetch * kOps>();
+  __builtin_amdgcn_s_barrier();
   // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g.
   v4i blo[NT], bhi[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    const v4i* src = reinterpret_cast<const v4i*>(qpack + (int64_t)(16 * j + c) * 128 + 32 * g);
+    const v4i* src = reinterpret_cast<const v4i*>(s_query) + (16 * j + c) * 8 + 2 * g;
     blo[j] = src[0];
     bhi[j] = src[1];
   }
-  // Complete every load issued so far (the compiler's waits for its own
-  // loads here also cover the older LDS-destination ones).
-  use_here(dtab);
-  use_here(offv);
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    use_here(blo[j]);
-    use_here(bhi[j]);
-  }
-  vm_wait_lds<0>();
 
   // Current tile, read back from the ring one step ahead of its use.
   vm_wait_lds<kRingWait>();
   v4u w = s_codes[wave][0][lane];
-  uint32_t sv = kTS ? s_scales[wave][0][lane] : 0u;
-
-  // Compute cursor: the tile whose MFMAs are issued in this step ...
-  int cp_k = 0;
-  uint32_t cp_t = 0u, cp_e = first_end;
-  // ... and the document of the tile whose epilogue runs in this step.
-  int pv_k = 0;
-  bool pv_last = false;
+  v4u sv = kTS ? *reinterpret_cast<const v4u*>(&s_scales[wave][0][0] + 4 * g) : (v4u){0u, 0u, 0u, 0u};
 
   float m[NT];
 #pragma unroll
@@ -240,8 +199,9 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
       m[j] = fmaxf(fmaxf(fmaxf(m[j], x0), x1), fmaxf(x2, x3));
     }
   };
-  // Document end: per-row maxima over the four lane groups, then the score.
-  auto finish = [&](int k) {
+  // Document end: per-row maxima over the four lane groups, then the score of
+  // local document `local`.
+  auto finish = [&](int local) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) m[j] = max_over_groups(m[j]);
     if (g == 0) {
@@ -249,19 +209,25 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
       for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = m[j];
     }
     wave_sync_lds();
-    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + doc_local(k), p.score_stride);
+    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride);
     wave_sync_lds();
 #pragma unroll
     for (int j = 0; j < NT; ++j) m[j] = kNegInf;
   };
 
-  // One pipeline step for the tile in `w` (ring slot `slot`): refill of that
+  // Per-tile entries (scalar loads one step ahead): `meta` describes the
+  // tile in `w`, `iss` is the start of the tile kPrefetch steps ahead.
+  uint64_t meta = tt[0], iss = tt[kPrefetch];
+  int slot = 0;
+  int pv_local = 0;
+  bool pv_last = false;
+
+  // One pipeline step for tile i (in `w`, ring slot `slot`): refill of that
   // slot, read-back of the next tile, then the tile's MFMAs interleaved with
   // the epilogue of the previous tile (accumulator set par ^ 1).  Only two
-  // copies of the step are unrolled (the ring slot is a runtime value) to keep
-  // the loop within the instruction cache.
-  int slot = 0;
-  auto step = [&](int par, bool has_prev) {
+  // copies of the step are unrolled (the ring slot is a runtime value) to
+  // keep the loop within the instruction cache.
+  auto step = [&](int i, int par, bool has_prev) {
     v4i lo, hi;
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
@@ -270,14 +236,17 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
     }
     float s0 = 0.0625f, s1 = 0.0625f, s2 = 0.0625f, s3 = 0.0625f;
     if (kTS) {
-      s0 = __uint_as_float(quad_broadcast<0>(sv)) * 0.0625f;
-      s1 = __uint_as_float(quad_broadcast<1>(sv)) * 0.0625f;
-      s2 = __uint_as_float(quad_broadcast<2>(sv)) * 0.0625f;
-      s3 = __uint_as_float(quad_broadcast<3>(sv)) * 0.0625f;
+      s0 = __uint_as_float(sv.x);
+      s1 = __uint_as_float(sv.y);
+      s2 = __uint_as_float(sv.z);
+      s3 = __uint_as_float(sv.w);
     }
-    // Rows of this tile past a short document are masked: their accumulators
+    const uint32_t mhi = (uint32_t)(meta >> 32);
+    const uint32_t rows = (mhi & 31u) + 1u;
+    const bool last = (mhi >> 5) & 1u;
+    const int local = (int)(mhi >> 8);
+    // Rows of a tile past a short document are masked: their accumulators
     // start at -2^30 (|16 * dot| < 2^22) and their scales are +inf.
-    const uint32_t rows = cp_e - cp_t < 16u ? cp_e - cp_t : 16u;
     v4i cinit = (v4i){0, 0, 0, 0};
     if (rows < 16u) {
       const uint32_t r0 = 4u * (uint32_t)g;
@@ -295,12 +264,13 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
     sc[par][3] = s3;
     // The slot's contents are in registers before the refill may land.
     lds_read_done(w, sv);
-    issue(slot);
+    load_tile(slot, (uint32_t)iss);
+    const uint64_t meta_n = tt[i + 1], iss_n = tt[i + 1 + kPrefetch];
     // Next tile: wait for its slot and read it back (consumed next step).
     slot = slot + 1 == kPrefetch ? 0 : slot + 1;
     vm_wait_lds<kRingWait>();
     w = s_codes[wave][slot][lane];
-    if (kTS) sv = s_scales[wave][slot][lane];
+    if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
@@ -314,45 +284,39 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
       }
-      if (pv_last) finish(pv_k);
+      if (pv_last) finish(pv_local);
     }
-    // Advance the compute cursor past this tile.
-    const bool last = cp_t + 16u >= cp_e;
-    pv_k = cp_k;
     pv_last = last;
-    if (last) {
-      ++cp_k;
-      cp_t = cp_e;
-      cp_e = cp_k < n_ne ? doc_end(cp_k) : cp_e;
-    } else {
-      cp_t = cp_t + 32u <= cp_e ? cp_t + 16u : cp_e - 16u;
-    }
+    pv_local = local;
+    meta = meta_n;
+    iss = iss_n;
   };
 
   if (ntiles > 0) {
     // Tile i lives in ring slot i % kPrefetch and accumulator set i & 1.
-    step(0, false);
+    step(0, 0, false);
     int i = 1;
     for (; i + 2 <= ntiles; i += 2) {
-      step(1, true);
-      step(0, true);
+      step(i, 1, true);
+      step(i + 1, 0, true);
     }
     if (i < ntiles) {
-      step(1, true);
+      step(i, 1, true);
       epilogue_max(1);
     } else {
       epilogue_max(0);
     }
-    finish(pv_k);  // the last tile always ends a document
+    finish(pv_local);  // the last tile always ends a document
   }
   // No LDS-destination load may still be in flight when the wave ends.
   vm_wait_lds<0>();
 
   // Empty documents score 0 (lane d owns local document d).
   if (has_empty) {
-    const uint64_t next = ((uint64_t)(uint32_t)__shfl_down((int)(uint32_t)(offv >> 32), 1) << 32) |
-                          (uint32_t)__shfl_down((int)(uint32_t)offv, 1);
-    if (lane < ndocs && next == offv) {
+    const int64_t off = lane <= ndocs ? offsets[d0 + lane] : 0;
+    const int64_t next = ((int64_t)__shfl_down((int)(uint32_t)((uint64_t)off >> 32), 1) << 32) |
+                         (uint32_t)__shfl_down((int)(uint32_t)(uint64_t)off, 1);
+    if (lane < ndocs && next == off) {
       for (int b = 0; b < p.batch; ++b) scores[(int64_t)b * p.score_stride + d0 + lane] = 0.0f;
     }
   }
@@ -363,8 +327,8 @@ static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_
   const dim3 grid((unsigned)blocks), block(kScanThreads);
   switch (nt) {
 #define MSIM_SCAN_CASE(N)                                                                           \
-  int8q_scan_kernel<N, kTS><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale, a.offsets,        \
-                                                        a.wave_info, a.doc_table, a.qpack, a.qscale, \
+  int8q_scan_kernel<N, kTS><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
+                                                        a.wave_info, a.tile_table, a.qpack, a.qscale, \
                                                         a.scores)
     case 1: MSIM_SCAN_CASE(1); break;
     case 2: MSIM_SCAN_CASE(2); break;
@@ -380,9 +344,10 @@ static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_
 
 hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream) {
   const int rows = args.batch * args.query_tokens;
-  if (rows <= 0 || rows > 128 || args.num_waves <= 0) return hipErrorInvalidValue;
+  if (rows <= 0 || rows > 128 || args.num_waves <= 0 || args.num_waves % kScanWaves != 0)
+    return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
-  const int64_t blocks = (args.num_waves + kScanWaves - 1) / kScanWaves;
+  const int64_t blocks = args.num_waves / kScanWaves;
   if (token_scale) launch_scan_nt<true>(args, nt, blocks, stream);
   else launch_scan_nt<false>(args, nt, blocks, stream);
   return hipGetLastError();

@@ -43,49 +43,44 @@ hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int
 //   [0] d0          first document
 //   [1] ndocs       documents [d0, d0 + ndocs)
 //   [2] T0, [3] T1  token range of the wave (offsets[d0], offsets[d0 + ndocs]),
-//                   with (T1 - T0) * 64 < 2^32
-//   [4] ntiles      sum over documents of ceil(len / 16)
-//   [5] n_ne        non-empty documents
-//   [6] tab0        index of the wave's first entry in the document table
-//   [7] end of the first non-empty document relative to T0 (low 32 bits),
-//       1 << 32 if the wave has empty documents
-// The document table holds, per non-empty document in order, (end - T0) in
-// the low 32 bits and the document's index relative to d0 in the high bits.
+//                   with (T1 - T0) * 64 < 2^31
+//   [4] ntiles      16-token tiles of the wave: sum over documents of ceil(len / 16)
+//   [5] tab0        index of the wave's first entry in the tile table
+//   [6] has_empty   the wave has empty documents
+// The table is padded to whole workgroups with waves of no tiles.  Tile table
+// entries (one per tile, then kScanPrefetch + 1 padding entries per wave):
+// low 32 bits the tile's first token relative to T0 (kScanPastEnd for
+// padding), then (rows - 1) in bits 32..36, "last tile of its document" in
+// bit 37 and the document's index relative to d0 in bits 40..47.
 constexpr int kWaveInfoWords = 8;
 constexpr int kScanMaxDocsPerWave = 63;
-// Ring depth of the scan (tiles in flight per wave) and the per-wave ring
-// table: the first kScanPrefetch tile starts (relative to T0; kScanPastEnd
-// past the last tile), then the load cursor after them: document index,
-// next tile start, end of that document.
+constexpr int kScanWavesPerGroup = 4;
 #ifndef MSIM_SCAN_PREFETCH
 #define MSIM_SCAN_PREFETCH 8
 #endif
-constexpr int kScanPrefetch = MSIM_SCAN_PREFETCH;
-constexpr int kScanRingWords = kScanPrefetch + 3;
-constexpr uint32_t kScanPastEnd = 0x3FFFFF0u;  // (kScanPastEnd + 15) * 64 + 48 < 2^32
+constexpr int kScanPrefetch = MSIM_SCAN_PREFETCH;  // ring depth: tiles in flight per wave
+constexpr uint32_t kScanPastEnd = 0x3FFFFF0u;      // (kScanPastEnd + 15) * 64 + 48 < 2^32
 struct ScanArgs {
-  const uint8_t* codes;       // [num_tokens, 64] int4 nibbles
-  const float* token_scale;   // [num_tokens] or nullptr (tensor scale)
-  const int64_t* offsets;     // [num_docs + 1]
-  const int64_t* wave_info;   // [num_waves, kWaveInfoWords]
-  const uint64_t* doc_table;  // per-wave non-empty document ends
-  const uint32_t* ring_starts; // [num_waves, kScanRingWords]
-  int64_t num_waves;
-  const int8_t* qpack;        // >= 16 * ceil(rows / 16) rows of MFMA B-order int8 codes
-  const float* qscale;        // per-row query scale, same row count
-  int32_t batch;              // batch rows of this pass (batch * query_tokens <= 128)
+  const uint8_t* codes;         // [num_tokens, 64] int4 nibbles
+  const float* token_scale16;   // [num_tokens] token scales / 16, or nullptr (tensor scale)
+  const int64_t* offsets;       // [num_docs + 1]
+  const int64_t* wave_info;     // [num_waves, kWaveInfoWords]
+  const uint64_t* tile_table;   // per-wave tile entries
+  int64_t num_waves;            // a multiple of kScanWavesPerGroup
+  const int8_t* qpack;          // >= rows + 128 rows of MFMA B-order int8 codes (zero past rows)
+  const float* qscale;          // per-row query scale, same row count
+  int32_t batch;                // batch rows of this pass (batch * query_tokens <= 128)
   int32_t query_tokens;
-  double scale;               // tensor scale (1.0 for per-token corpora)
-  float* scores;              // [batch, score_stride]
+  double scale;                 // tensor scale (1.0 for per-token corpora)
+  float* scores;                // [batch, score_stride]
   int64_t score_stride;
 };
-// Builds the wave table and document table for `waves` requested waves
-// (the result may hold more rows: ranges are split at kScanMaxDocsPerWave
-// documents and at 2^25 tokens).
-void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves,
-                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& doc_table,
-                       std::vector<uint32_t>& ring_starts);
 hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream);
+// Builds the wave table and tile table for `waves` requested waves (the
+// result may hold more rows: ranges are split at kScanMaxDocsPerWave
+// documents and 2^25 tokens, and padded to whole workgroups).
+void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves,
+                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table);
 
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a
