@@ -244,38 +244,47 @@ int64_t scan_waves(const msim_int4_docs* h) {
   return std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
 }
 
+// Score the query quantised in the workspace: the MFMA scan for passes of at
+// most 128 query rows, the row-maxima path beyond.
+void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* d_scores,
+                     hipStream_t stream) {
+  if (query_tokens == 0 || h->num_docs == 0 || query_tokens > 128) {
+    score_int8q(h, batch, query_tokens, d_scores, stream);
+    return;
+  }
+  if (h->quantized_rows != batch * query_tokens)
+    throw InvalidArgument("no quantised query of this shape: call quantize first with the same batch and query_tokens");
+  build_wave_info(h, scan_waves(h));
+  ScanArgs a{};
+  a.codes = h->packed.as<uint8_t>();
+  a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
+  a.offsets = h->offsets.as<int64_t>();
+  a.wave_info = h->wave_info.as<int64_t>();
+  a.tile_table = h->tile_table.as<uint64_t>();
+  a.num_waves = h->num_scan_waves;
+  a.query_tokens = (int32_t)query_tokens;
+  a.scale = h->scale;
+  a.score_stride = h->num_docs;
+  const int64_t per_pass = 128 / query_tokens;
+  for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
+    const int64_t nb = std::min(per_pass, batch - b0);
+    a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;
+    a.qscale = h->qscale.as<float>() + b0 * query_tokens;
+    a.batch = (int32_t)nb;
+    a.scores = d_scores + b0 * h->num_docs;
+    check_hip(launch_int8q_scan(a, h->has_token_scale, stream), "launch int8q scan kernel");
+  }
+}
+
 // Full int8-query search: scores of every document into d_scores [B, N] and,
 // when k > 0, the top-k of each batch row into d_top_s / d_top_i [B, k].
-// Query quantisation, the scan (one launch per pass of <= 128 query rows) and
-// the selection are separate launches on one stream.
+// Quantisation, the scan and the selection are separate launches on one
+// stream.
 void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                   float* d_scores, int64_t k, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   if (batch == 0) return;
   quantize_int8q(h, d_query, batch, query_tokens, stream);
-  if (query_tokens == 0 || h->num_docs == 0 || query_tokens > 128) {
-    score_int8q(h, batch, query_tokens, d_scores, stream);
-  } else {
-    build_wave_info(h, scan_waves(h));
-    ScanArgs a{};
-    a.codes = h->packed.as<uint8_t>();
-    a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
-    a.offsets = h->offsets.as<int64_t>();
-    a.wave_info = h->wave_info.as<int64_t>();
-    a.tile_table = h->tile_table.as<uint64_t>();
-    a.num_waves = h->num_scan_waves;
-    a.query_tokens = (int32_t)query_tokens;
-    a.scale = h->scale;
-    a.score_stride = h->num_docs;
-    const int64_t per_pass = 128 / query_tokens;
-    for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
-      const int64_t nb = std::min(per_pass, batch - b0);
-      a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;
-      a.qscale = h->qscale.as<float>() + b0 * query_tokens;
-      a.batch = (int32_t)nb;
-      a.scores = d_scores + b0 * h->num_docs;
-      check_hip(launch_int8q_scan(a, h->has_token_scale, stream), "launch int8q scan kernel");
-    }
-  }
+  score_quantized(h, batch, query_tokens, d_scores, stream);
   if (k > 0)
     check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),
               "launch int8q topk selection kernel");
@@ -502,7 +511,7 @@ extern "C" int msim_int4_score_int8q_async(msim_int4_docs* h, int64_t batch, int
     require_shape(batch, query_tokens);
     if (batch == 0 || h->num_docs == 0) return;
     select_device(h->device);
-    score_int8q(h, batch, query_tokens, d_out, as_stream(stream));
+    score_quantized(h, batch, query_tokens, d_out, as_stream(stream));
   });
 }
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace msim {
 
@@ -120,6 +121,27 @@ __device__ __forceinline__ void wave_sync_lds() {
 template <int I>
 __device__ __forceinline__ uint32_t quad_broadcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, I * 0x55, 0xF, 0xF, false);
+}
+
+// Whole-wave reduction: DPP quad butterflies and row rotations by 4 and 8
+// reduce each row of 16 lanes, then the four row results are combined from
+// lanes 0, 16, 32 and 48.  The result is wave-uniform.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  static_assert(sizeof(T) == 4, "32-bit values");
+  auto dpp = [](T x, auto ctrl) -> T {
+    return __builtin_bit_cast(T, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), decltype(ctrl)::value, 0xF, 0xF, true));
+  };
+  v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  v = op(v, dpp(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+  v = op(v, dpp(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+  const int x = __builtin_bit_cast(int, v);
+  const T r0 = __builtin_bit_cast(T, __builtin_amdgcn_readlane(x, 0));
+  const T r1 = __builtin_bit_cast(T, __builtin_amdgcn_readlane(x, 16));
+  const T r2 = __builtin_bit_cast(T, __builtin_amdgcn_readlane(x, 32));
+  const T r3 = __builtin_bit_cast(T, __builtin_amdgcn_readlane(x, 48));
+  return op(op(r0, r1), op(r2, r3));
 }
 
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(a, fmaxf(b, c)); }

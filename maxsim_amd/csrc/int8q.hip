@@ -44,15 +44,11 @@ __global__ __launch_bounds__(256) void quantize_query_int8_kernel(
     return;
   }
   const float2 v = reinterpret_cast<const float2*>(query + row * 128)[lane];
-  float m = fmaxf(fabsf(v.x), fabsf(v.y));
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const float m = wave_reduce(fmaxf(fabsf(v.x), fabsf(v.y)), [](float x, float y) { return fmaxf(x, y); });
   const float s = m == 0.0f ? 1.0f : __fdiv_rn(m, 127.0f);
   const int a = max(-127, min(127, (int)rintf(__fdiv_rn(v.x, s))));
   const int b = max(-127, min(127, (int)rintf(__fdiv_rn(v.y, s))));
-  int sum = a + b;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
   dst[32 * g + i] = (int8_t)a;
   dst[32 * g + 16 + i] = (int8_t)b;
   if (lane == 0) {

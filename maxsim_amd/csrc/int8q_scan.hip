@@ -26,7 +26,7 @@
 //    float(acc) * (s_t / 16) rounds the same real number as float(dot) * s_t;
 //  * software pipelined: the MFMAs of tile i are issued before the VALU
 //    epilogue (scale, running max) of tile i - 1;
-//  * at a document end: cross-lane max with permlane swaps and numpy's
+//  * at a document end: cross-lane max over the four lane groups and numpy's
 //    float64 pairwise sum over query tokens.
 #include "common.hpp"
 #include "internal.hpp"
@@ -40,10 +40,8 @@ static_assert(kPrefetch >= 2, "ring of at least two tiles");
 
 // Maximum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
 __device__ __forceinline__ float max_over_groups(float v) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  return fmaxf(v, __shfl_xor(v, 32));
 }
 
 // out[b * stride] = f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale), b < batch.

@@ -1,6 +1,7 @@
 // topk.hip -- stand-alone block top-k: one 1024-thread workgroup per score row.
 // Selection algorithm and order: topk_block.hpp (reference order cu:1629-1692,
 // _api.py:732-735).
+#include "common.hpp"
 #include "internal.hpp"
 #include "topk_block.hpp"
 
@@ -20,13 +21,176 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
                                           out_ids + b * k, sm);
 }
 
+// ------------------------------------------------------------- small k
+// k <= kSmallTopkMaxK and n <= THREADS * kSmallEPT: every element stays in
+// registers as a 64-bit key (order-preserving score bits above the inverted
+// position, so a larger key is a higher score or, on a tie, a lower
+// position) and the k results come from k rounds of a block-wide maximum.
+constexpr int kSmallTopkMaxK = 32;
+constexpr int kSmallEPT = 16;
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_update_u64(uint64_t old, uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)old, (int)(uint32_t)v, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(old >> 32), (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Maximum over the wave, wave-uniform: DPP butterflies and rotations within
+// rows of 16 lanes, row broadcasts 15 and 31 into lane 63, then readlane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t o = dpp_u64<0xB1>(v);  // quad_perm [1,0,3,2]
+  v = v > o ? v : o;
+  o = dpp_u64<0x4E>(v);  // quad_perm [2,3,0,1]
+  v = v > o ? v : o;
+  o = dpp_u64<0x124>(v);  // row_ror:4
+  v = v > o ? v : o;
+  o = dpp_u64<0x128>(v);  // row_ror:8
+  v = v > o ? v : o;
+  o = dpp_update_u64<0x142, 0xA>(v, v);  // row_bcast:15 into rows 1 and 3
+  v = v > o ? v : o;
+  o = dpp_update_u64<0x143, 0xC>(v, v);  // row_bcast:31 into rows 2 and 3
+  v = v > o ? v : o;
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+}
+
+// Maximum of a 32-bit value over the wave (wave-uniform), DPP only.
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Sorts a lane's E keys into descending order (odd-even transposition
+// network, E rounds of independent compare-exchanges).
+template <int E>
+__device__ __forceinline__ void lane_sort_desc(uint64_t (&key)[E]) {
+#pragma unroll
+  for (int round = 0; round < E; ++round) {
+#pragma unroll
+    for (int i = round & 1; i + 1 < E; i += 2) {
+      const uint64_t a = key[i], b = key[i + 1];
+      key[i] = a > b ? a : b;
+      key[i + 1] = a > b ? b : a;
+    }
+  }
+}
+
+// The k largest of the keys held by the wave (E per lane), largest first,
+// into out[0..k) (lane 0 writes).  Keys of 0 are empty slots.  Each lane's
+// keys are sorted first, so a round is one wave maximum over the lanes'
+// heads plus a shift in the winning lane; only a tie on the score half
+// needs the full 64-bit reduction.
+template <int E>
+__device__ __forceinline__ void wave_select(uint64_t (&key)[E], int k, uint64_t* out) {
+  lane_sort_desc(key);
+  for (int r = 0; r < k; ++r) {
+    const uint64_t head = key[0];
+    const uint32_t hs = (uint32_t)(head >> 32);
+    const uint32_t top = wave_max_u32_dpp(hs);
+    const uint64_t holders = __ballot(hs == top);
+    uint64_t best;
+    if (__popcll(holders) == 1) {
+      const int owner = __ffsll((unsigned long long)holders) - 1;
+      best = ((uint64_t)top << 32) | (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)head, owner);
+    } else {
+      best = wave_max_u64(head);
+    }
+    if (lane_id() == 0) out[r] = best;
+    if (best != 0 && head == best) {  // the one lane holding it drops it
+#pragma unroll
+      for (int e = 0; e + 1 < E; ++e) key[e] = key[e + 1];
+      key[E - 1] = 0u;
+    }
+  }
+}
+
+// One workgroup per row: each wave selects the k best of its kWave * kSmallEPT
+// elements, then wave 0 selects the k best of those candidates.  No
+// workgroup barrier inside the selection rounds.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void topk_small_kernel(const float* __restrict__ scores, int64_t n,
+                                                            int64_t row_stride, int32_t k,
+                                                            const int64_t* __restrict__ id_map,
+                                                            float* __restrict__ out_scores,
+                                                            int64_t* __restrict__ out_ids) {
+  constexpr int kWaves = THREADS / kWave;
+  __shared__ uint64_t s_cand[kWaves * kSmallTopkMaxK];
+  __shared__ uint64_t s_best[kSmallTopkMaxK];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t b = blockIdx.x;
+  const float* row = scores + b * row_stride;
+  // Bounds-checked loads (positions past n read zero), all issued first.
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
+  const int base = wave * kWave * kSmallEPT + lane;
+  float v[kSmallEPT];
+#pragma unroll
+  for (int e = 0; e < kSmallEPT; ++e) v[e] = __uint_as_float(load_b32(rsrc, (base + e * kWave) * 4));
+  uint64_t key[kSmallEPT];
+#pragma unroll
+  for (int e = 0; e < kSmallEPT; ++e) {
+    const int i = base + e * kWave;
+    key[e] = i < n ? ((uint64_t)score_key(v[e]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0u;
+  }
+  wave_select(key, k, s_cand + wave * kSmallTopkMaxK);
+  __syncthreads();
+  // Merge the waves' sorted lists (one thread, k steps over kWaves heads).
+  if (tid == 0) {
+    int pos[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) pos[w] = 0;
+    for (int r = 0; r < k; ++r) {
+      uint64_t best = 0;
+      int from = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const uint64_t h = pos[w] < k ? s_cand[w * kSmallTopkMaxK + pos[w]] : 0u;
+        if (h > best) {
+          best = h;
+          from = w;
+        }
+      }
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) pos[w] += w == from ? 1 : 0;
+      s_best[r] = best;
+    }
+  }
+  __syncthreads();
+  if (tid < k) {
+    const int64_t pos = (int64_t)(0xFFFFFFFFu - (uint32_t)s_best[tid]);
+    out_scores[b * k + tid] = row[pos];
+    out_ids[b * k + tid] = id_map ? id_map[b * n + pos] : pos;
+  }
+}
+
 hipError_t launch_topk(const float* d_scores, int64_t batch, int64_t n, int64_t row_stride,
                        int64_t k, const int64_t* d_id_map, float* d_out_scores,
                        int64_t* d_out_ids, hipStream_t stream) {
   if (batch == 0 || k == 0) return hipSuccess;
   if (k > kTopkMaxK || k > n) return hipErrorInvalidValue;
-  topk_kernel<<<dim3((unsigned)batch), dim3(kTopkThreads), 0, stream>>>(
-      d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
+  if (k <= kSmallTopkMaxK && n <= 256 * kSmallEPT) {
+    topk_small_kernel<256><<<dim3((unsigned)batch), dim3(256), 0, stream>>>(
+        d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
+  } else if (k <= kSmallTopkMaxK && n <= 1024 * kSmallEPT) {
+    topk_small_kernel<1024><<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(
+        d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
+  } else {
+    topk_kernel<<<dim3((unsigned)batch), dim3(kTopkThreads), 0, stream>>>(
+        d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
+  }
   return hipGetLastError();
 }
 
