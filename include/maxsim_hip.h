@@ -183,6 +183,16 @@ int msim_binary_topk_batch(msim_binary_docs* h, const float* query, int64_t batc
                            int64_t query_tokens, int64_t dim, int64_t k, double scale,
                            int use_scale_vector, int use_token_scale, float* out_scores,
                            int64_t* out_indices);
+/* maxsim_batch_int8q / topk_batch_int8q (cu:2213-2268): the query is
+ * quantised per row to int8 as q * (1 / sigma) (cu:1328-1366) and scored as
+ * 2 (q8 . bits) - sum(q8) (cu:1368-1447); dim 128 only. */
+int msim_binary_maxsim_batch_int8q(msim_binary_docs* h, const float* query, int64_t batch,
+                                   int64_t query_tokens, int64_t dim, double scale,
+                                   int use_scale_vector, int use_token_scale, float* out);
+int msim_binary_topk_batch_int8q(msim_binary_docs* h, const float* query, int64_t batch,
+                                 int64_t query_tokens, int64_t dim, int64_t k, double scale,
+                                 int use_scale_vector, int use_token_scale, float* out_scores,
+                                 int64_t* out_indices);
 /* score_batch / score_candidates_batch with the generalized reducers
  * (cu:2005-2067, score_impl).  scale_vector_override: NULL or f32[N]. */
 int msim_binary_score(msim_binary_docs* h, const float* query, int64_t batch,

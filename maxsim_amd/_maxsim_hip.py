@@ -240,6 +240,218 @@ class CudaInt4PackedDocs:
         return int(self._props().workspace_bytes)
 
 
+class CudaPackedDocs:
+    """Resident sign-bit corpus (reference: CudaPackedDocs, cu:1872-2675).
+
+    Every scoring method runs the MFMA kernels of score.hip: fp32 queries are
+    split into three int8 limbs, int8 queries (``*_int8q``) use one, and
+    sign-bit queries (``hamming_batch`` / ``topk_hamming``) are exact +-1
+    dot products, i.e. dim - 2 popcount(q ^ d)."""
+
+    def __init__(self, packed, offsets, dim: int):
+        lib = _native.load()
+        packed = _u8(packed)
+        offsets = _i64(offsets)
+        if packed.ndim != 2:
+            raise ValueError("packed must have shape [num_doc_tokens, dim / 8]")
+        if offsets.ndim != 1:
+            raise ValueError("offsets must be a 1-D array")
+        handle = ctypes.c_void_p()
+        check(lib.msim_binary_create(ptr(packed), packed.shape[0], packed.shape[1], ptr(offsets),
+                                     offsets.shape[0], int(dim), ctypes.byref(handle)))
+        self._lib = lib
+        self._h = handle
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.msim_binary_destroy(h)
+            self._h = None
+
+    # ---------------------------------------------------------- residency
+    def set_scale_vector(self, scale):
+        v = _f32(scale)
+        if v.ndim != 1:
+            raise ValueError("scale vector must have shape [num_docs]")
+        check(self._lib.msim_binary_set_scale_vector(self._h, ptr(v), v.shape[0]))
+
+    def clear_scale_vector(self):
+        check(self._lib.msim_binary_clear_scale_vector(self._h))
+
+    def set_token_scale_vector(self, token_scales):
+        v = _f32(token_scales)
+        if v.ndim != 1:
+            raise ValueError("token scale vector must have shape [num_doc_tokens]")
+        check(self._lib.msim_binary_set_token_scale(self._h, ptr(v), v.shape[0]))
+
+    def clear_token_scale_vector(self):
+        check(self._lib.msim_binary_clear_token_scale(self._h))
+
+    # ------------------------------------------------------------ scoring
+    def maxsim_batch(self, query, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        q = _query3(query)
+        out = np.empty((q.shape[0], self.num_docs), np.float32)
+        check(self._lib.msim_binary_maxsim_batch(self._h, ptr(q), *q.shape, float(scale), int(bool(use_scale_vector)),
+                                                 int(bool(use_token_scale)), ptr(out)))
+        return out
+
+    def _topk(self, fn, query, k, scale, use_scale_vector, use_token_scale):
+        q = _query3(query)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(fn(self._h, ptr(q), *q.shape, k, float(scale), int(bool(use_scale_vector)),
+                 int(bool(use_token_scale)), ptr(scores), ptr(indices)))
+        return scores, indices
+
+    def topk_batch(self, query, k, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        return self._topk(self._lib.msim_binary_topk_batch, query, k, scale, use_scale_vector, use_token_scale)
+
+    def topk_lut_batch(self, query, k, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        """Same scores as topk_batch (the reference's LUT kernel is a different
+        evaluation of the same sum); dim 128 only, as cu:2165-2211."""
+        if self.dim != 128:
+            raise ValueError("topk_lut_batch currently requires dim=128")
+        return self.topk_batch(query, k, scale, use_scale_vector, use_token_scale)
+
+    def streaming_topk_batch(self, query, k, scale=1.0, use_scale_vector=False):
+        """Top-k without a token scale (cu:2270-2329)."""
+        return self.topk_batch(query, k, scale, use_scale_vector, False)
+
+    def topk_centroid_batch(self, query, weights, k, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        """Top-k of the query with every dim multiplied by weights[dim] (cu:2111-2163)."""
+        q = _query3(query)
+        w = _f32(weights)
+        if w.ndim != 1 or w.shape[0] != self.dim:
+            raise ValueError("weights must have shape [dim]")
+        return self.topk_batch(q * w[None, None, :], k, scale, use_scale_vector, use_token_scale)
+
+    def maxsim_batch_int8q(self, query, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        q = _query3(query)
+        out = np.empty((q.shape[0], self.num_docs), np.float32)
+        check(self._lib.msim_binary_maxsim_batch_int8q(self._h, ptr(q), *q.shape, float(scale),
+                                                       int(bool(use_scale_vector)), int(bool(use_token_scale)),
+                                                       ptr(out)))
+        return out
+
+    def topk_batch_int8q(self, query, k, scale=1.0, use_scale_vector=False, use_token_scale=False):
+        return self._topk(self._lib.msim_binary_topk_batch_int8q, query, k, scale, use_scale_vector,
+                          use_token_scale)
+
+    def _score(self, query, candidate_indices, reducer, query_weights, temperature, scale, use_scale_vector,
+               use_token_scale, scale_vector_override):
+        q = _query3(query)
+        w, wnd, w0, w1 = _weights(query_weights)
+        cand = None if candidate_indices is None else _candidates(candidate_indices)
+        targets = self.num_docs if cand is None else cand.shape[0]
+        override = None
+        if scale_vector_override is not None:
+            override = _f32(scale_vector_override)
+            if override.ndim != 1 or override.shape[0] != self.num_docs:
+                raise ValueError("scale vector must have shape [num_docs]")
+        if not isinstance(reducer, str):
+            raise ValueError("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'")
+        out = np.empty((q.shape[0], targets), np.float32)
+        check(self._lib.msim_binary_score(
+            self._h, ptr(q), *q.shape, reducer.encode(), ptr(w), wnd, w0, w1, float(temperature), float(scale),
+            int(bool(use_scale_vector)), int(bool(use_token_scale)), ptr(override), ptr(cand),
+            0 if cand is None else cand.shape[0], ptr(out)))
+        return out
+
+    def score_batch(self, query, reducer="maxsim", query_weights=None, temperature=1.0, scale=1.0,
+                    use_scale_vector=False, use_token_scale=False, scale_vector_override=None):
+        return self._score(query, None, reducer, query_weights, temperature, scale, use_scale_vector,
+                           use_token_scale, scale_vector_override)
+
+    def score_candidates_batch(self, query, candidate_indices, reducer="maxsim", query_weights=None,
+                               temperature=1.0, scale=1.0, use_scale_vector=False, use_token_scale=False,
+                               scale_vector_override=None):
+        return self._score(query, candidate_indices, reducer, query_weights, temperature, scale,
+                           use_scale_vector, use_token_scale, scale_vector_override)
+
+    # ------------------------------------------------- sign-bit queries
+    def hamming_batch(self, qbits):
+        """int32 [B, N]: sum_q max_t (dim - 2 popcount(qbits[b, q] ^ d_t)) for
+        sign-bit queries u8 [B, Q, dim / 8] in pack_signs order."""
+        qb = _u8(qbits)
+        if qb.ndim != 3 or qb.shape[2] != self.dim // 8:
+            raise ValueError("qbits must have shape [batch, query_tokens, dim / 8]")
+        out = np.empty((qb.shape[0], self.num_docs), np.int32)
+        check(self._lib.msim_binary_hamming_batch(self._h, ptr(qb), qb.shape[0], qb.shape[1], self.dim, ptr(out)))
+        return out
+
+    def topk_hamming(self, qbits, k):
+        qb = _u8(qbits)
+        if qb.ndim != 3 or qb.shape[2] != self.dim // 8:
+            raise ValueError("qbits must have shape [batch, query_tokens, dim / 8]")
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        scores = np.empty((qb.shape[0], k), np.float32)
+        indices = np.empty((qb.shape[0], k), np.int64)
+        check(self._lib.msim_binary_topk_hamming(self._h, ptr(qb), qb.shape[0], qb.shape[1], self.dim, k,
+                                                 ptr(scores), ptr(indices)))
+        return scores, indices
+
+    def topk_hamming_async(self, qbits, k, scores, indices, stream=None):
+        """Enqueue on device tensors: qbits u8[B, Q, 16], scores f32[B, k], indices i64[B, k]."""
+        b, q = int(qbits.shape[0]), int(qbits.shape[1])
+        check(self._lib.msim_binary_topk_hamming_async(self._h, ptr(qbits), b, q, int(k), ptr(scores),
+                                                       ptr(indices), _stream_ptr(stream)))
+
+    # --------------------------------------------------------- properties
+    def _props(self):
+        props = _native.BinaryProps()
+        check(self._lib.msim_binary_get_props(self._h, ctypes.byref(props)))
+        return props
+
+    @property
+    def dim(self) -> int:
+        return int(self._props().dim)
+
+    @property
+    def num_docs(self) -> int:
+        return int(self._props().num_docs)
+
+    @property
+    def num_tokens(self) -> int:
+        return int(self._props().num_tokens)
+
+    @property
+    def packed_size(self) -> int:
+        return int(self._props().packed_size)
+
+    @property
+    def has_scale_vector(self) -> bool:
+        return bool(self._props().has_scale_vector)
+
+    @property
+    def scale_vector_size(self) -> int:
+        return int(self._props().scale_vector_size)
+
+    @property
+    def has_token_scale_vector(self) -> bool:
+        return bool(self._props().has_token_scale_vector)
+
+    @property
+    def token_scale_vector_size(self) -> int:
+        return int(self._props().token_scale_vector_size)
+
+    @property
+    def resident_bytes(self) -> int:
+        return int(self._props().resident_bytes)
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(self._props().workspace_bytes)
+
+    @property
+    def maxsim_kernel_variant(self) -> str:
+        return "mfma_sign_i8"
+
+
 def _stream_ptr(stream):
     if stream is None:
         try:

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, list] = {
     "msim_binary_get_props": [c_vp, c_vp],
     "msim_binary_maxsim_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_dbl, c_int, c_int, c_vp],
     "msim_binary_topk_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_dbl, c_int, c_int, c_vp, c_vp],
+    "msim_binary_maxsim_batch_int8q": [c_vp, c_vp, c_i64, c_i64, c_i64, c_dbl, c_int, c_int, c_vp],
+    "msim_binary_topk_batch_int8q": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_dbl, c_int, c_int, c_vp, c_vp],
     "msim_binary_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl,
                           c_dbl, c_int, c_int, c_vp, c_vp, c_i64, c_vp],
     "msim_binary_hamming_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp],

@@ -2,7 +2,7 @@
 // input validation with the reference's messages, device workspaces and
 // kernel orchestration.  Handle semantics follow CudaInt4PackedDocs
 // (cuda_extension.cu:2677-3306) and CudaPackedDocs (cu:1872-2675).
-#include "capi_internal.hpp"
+#include "capi_handles.hpp"
 
 #include <cmath>
 #include <cstdlib>
@@ -92,37 +92,6 @@ extern "C" int msim_get_docs_per_wave(void) { return g_docs_per_wave; }
 
 // -------------------------------------------------------------- int4 handle
 
-struct msim_int4_docs {
-  int device = 0;
-  int64_t dim = 0;
-  int64_t num_docs = 0;
-  int64_t num_tokens = 0;
-  double scale = 1.0;
-  double residual_scale = 1.0;
-  uint64_t packed_size = 0;
-  uint64_t offsets_size = 0;
-  bool has_token_scale = false;
-  bool has_residual = false;
-  int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
-  std::vector<int64_t> host_offsets;
-  int64_t partition_waves = 0;    // wave count the cached scan table was built for
-  int64_t num_scan_waves = 0;     // rows of wave_info
-  DeviceBuffer wave_info, tile_table;
-  DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales;
-  // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
-  DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax, weights,
-      candidates;
-
-  uint64_t resident_bytes() const {
-    return packed_size + offsets_size * 8 + token_scales.cap + token_scales16.cap + residual_packed.cap +
-           residual_token_scales.cap;
-  }
-  uint64_t workspace_bytes() const {
-    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap +
-           top_indices.cap + rowmax.cap + weights.cap + candidates.cap + wave_info.cap + tile_table.cap;
-  }
-};
-
 namespace {
 
 void select_device(int device) { check_hip(hipSetDevice(device), "hipSetDevice"); }
@@ -138,6 +107,28 @@ void check_k(int64_t k, int64_t num_docs) {
 
 void check_int8q(const msim_int4_docs* h) {
   if (h->dim != 128) throw InvalidArgument("int8 query scoring currently requires dim=128");
+}
+
+// Upload `count` floats times `factor` (a power of two: exact).
+void upload_scaled(DeviceBuffer& dst, const float* src, int64_t count, float factor, const char* what) {
+  std::vector<float> scaled(src, src + count);
+  for (float& v : scaled) v *= factor;
+  dst.ensure(std::max<int64_t>(count * 4, 4), what);
+  if (count) check_hip(hipMemcpy(dst.ptr, scaled.data(), count * 4, hipMemcpyHostToDevice), what);
+}
+
+// int4 rows of row_bytes < 64 bytes widened to 64 bytes with zero nibbles
+// (zero codes add nothing to a dot product).
+void upload_codes128(DeviceBuffer& dst, const uint8_t* src, int64_t num_tokens, int64_t row_bytes,
+                     const char* what) {
+  if (row_bytes >= 64) {
+    dst.reset();
+    return;
+  }
+  std::vector<uint8_t> wide((size_t)std::max<int64_t>(num_tokens, 1) * 64, 0);
+  for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 64], src + t * row_bytes, (size_t)row_bytes);
+  dst.ensure(wide.size(), what);
+  check_hip(hipMemcpy(dst.ptr, wide.data(), wide.size(), hipMemcpyHostToDevice), what);
 }
 
 // Quantise d_query [B,Q,128] into the handle's query workspace.
@@ -337,6 +328,7 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
     if (h->packed_size)
       check_hip(hipMemcpy(h->packed.ptr, packed, h->packed_size, hipMemcpyHostToDevice), "copy int4 packed docs to device");
     check_hip(hipMemcpy(h->offsets.ptr, offsets, h->offsets_size * 8, hipMemcpyHostToDevice), "copy int4 offsets to device");
+    if (dim < 128) upload_codes128(h->codes128, packed, num_tokens, row_bytes, "int4 packed docs (128 dims)");
     *out = h.release();
   });
 }
@@ -358,14 +350,9 @@ extern "C" int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_s
     h->token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector");
     if (count)
       check_hip(hipMemcpy(h->token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 token scale vector to device");
-    // The int8-query scan multiplies 16 * dot by s / 16 (a power-of-two
-    // rescale, exact for normal floats).
-    std::vector<float> scaled(token_scales, token_scales + count);
-    for (float& v : scaled) v *= 0.0625f;
-    h->token_scales16.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector / 16");
-    if (count)
-      check_hip(hipMemcpy(h->token_scales16.ptr, scaled.data(), count * 4, hipMemcpyHostToDevice),
-                "copy int4 token scale vector / 16 to device");
+    // The MFMA kernels multiply 16 * dot by s / 16 (a power-of-two rescale,
+    // exact for normal floats).
+    upload_scaled(h->token_scales16, token_scales, count, 0.0625f, "int4 token scale vector / 16");
     h->has_token_scale = true;
   });
 }
@@ -390,9 +377,9 @@ extern "C" int msim_int4_set_residual(msim_int4_docs* h, const uint8_t* packed, 
     select_device(h->device);
     const size_t pbytes = (size_t)num_tokens * (size_t)row_bytes;
     h->residual_packed.ensure(std::max<size_t>(pbytes, 64), "hipMalloc resident int4 residual data");
-    h->residual_token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 residual token scales");
     if (pbytes) check_hip(hipMemcpy(h->residual_packed.ptr, packed, pbytes, hipMemcpyHostToDevice), "copy int4 residual data to device");
-    if (count) check_hip(hipMemcpy(h->residual_token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 residual token scales to device");
+    upload_codes128(h->residual128, packed, num_tokens, row_bytes, "int4 residual data");
+    upload_scaled(h->residual_token_scales16, token_scales, count, 0.0625f, "int4 residual token scales");
     h->residual_scale = scale;
     h->has_residual = true;
   });

@@ -1,0 +1,118 @@
+// capi_handles.hpp -- the resident corpus handles behind the C ABI and the
+// workspaces of the generalized scoring path (score.hip).
+#pragma once
+
+#include <vector>
+
+#include "capi_internal.hpp"
+
+namespace msim {
+
+// Device workspaces of one handle's generalized scoring calls (grow
+// monotonically, freed with the handle; cu:3057-3067).
+struct ScoreWorkspace {
+  DeviceBuffer qpack, colmul, qsum, weights, pooled, query, qbits;
+  DeviceBuffer full_info, full_tiles;  // cached whole-corpus tables
+  int64_t full_key = -1;               // wave count the cached tables were built for
+  int64_t full_waves = 0;              // waves in the cached table
+  DeviceBuffer cand_ids, cand_info, cand_tiles;
+  uint64_t bytes() const {
+    return qpack.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + query.cap + qbits.cap + full_info.cap +
+           full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap;
+  }
+};
+
+// Which query the generalized path scores.
+struct QueryInput {
+  const float* d_query = nullptr;    // fp32 [rows, 128] on the device, or
+  const uint8_t* d_qbits = nullptr;  // sign bits [rows, 16] (pack_signs order)
+  int limbs = 3;                     // 3: fp32 split into int8 limbs, 1: int8
+  bool recip = false;                // int8 rounding q * (1 / sigma) (binary int8q)
+};
+
+// The document streams and scales of one scoring call.
+struct DocStreams {
+  int doc = kDocInt4;
+  bool residual = false;
+  const uint8_t* codes = nullptr;
+  const float* tscale = nullptr;
+  float tmul = 1.0f;
+  const uint8_t* rcodes = nullptr;
+  const float* rtscale = nullptr;
+  float rmul = 1.0f;
+  const float* doc_scale = nullptr;
+  float scale = 1.0f;
+};
+
+// Candidate targets: none (every document), one list shared by all batch
+// rows, or one list of `count` per batch row.
+struct Targets {
+  const int64_t* host = nullptr;
+  int64_t count = 0;
+  bool per_row = false;
+};
+
+// Scores of `batch` x `query_tokens` query rows against the targets into
+// d_out[b * out_stride + t] (and d_iout[b * targets + t] as int32 if set).
+void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& host_offsets, int64_t num_tokens,
+                       const DocStreams& s, const QueryInput& q, int reducer, float temperature,
+                       int64_t batch, int64_t query_tokens, const float* h_row_weights, const Targets& t,
+                       float* d_out, int64_t out_stride, int32_t* d_iout, hipStream_t stream);
+
+}  // namespace msim
+
+struct msim_int4_docs {
+  int device = 0;
+  int64_t dim = 0;
+  int64_t num_docs = 0;
+  int64_t num_tokens = 0;
+  double scale = 1.0;
+  double residual_scale = 1.0;
+  uint64_t packed_size = 0;
+  uint64_t offsets_size = 0;
+  bool has_token_scale = false;
+  bool has_residual = false;
+  int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
+  std::vector<int64_t> host_offsets;
+  int64_t partition_waves = 0;    // wave count the cached scan table was built for
+  int64_t num_scan_waves = 0;     // rows of wave_info
+  msim::DeviceBuffer wave_info, tile_table;
+  msim::DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales16;
+  // Generalized path: codes padded to 64 bytes per token when dim < 128,
+  // per-token 1/16 when the corpus has no token scales.
+  msim::DeviceBuffer codes128, residual128, ones16;
+  // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
+  msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
+  msim::ScoreWorkspace ws;
+
+  uint64_t resident_bytes() const {
+    return packed_size + offsets_size * 8 + token_scales.cap + token_scales16.cap + residual_packed.cap +
+           residual_token_scales16.cap + codes128.cap + residual128.cap + ones16.cap;
+  }
+  uint64_t workspace_bytes() const {
+    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap + top_indices.cap +
+           rowmax.cap + wave_info.cap + tile_table.cap + ws.bytes();
+  }
+};
+
+struct msim_binary_docs {
+  int device = 0;
+  int64_t dim = 0;
+  int64_t num_docs = 0;
+  int64_t num_tokens = 0;
+  uint64_t packed_size = 0;
+  bool has_scale_vector = false;
+  bool has_token_scale = false;
+  std::vector<int64_t> host_offsets;
+  // codes padded to 16 bytes (128 dims) per token
+  msim::DeviceBuffer packed, offsets, scale_vector, token_scales, ones, scale_override;
+  msim::DeviceBuffer scores, top_scores, top_indices, iscores;
+  msim::ScoreWorkspace ws;
+
+  uint64_t resident_bytes() const {
+    return packed.cap + offsets.cap + scale_vector.cap + token_scales.cap + ones.cap;
+  }
+  uint64_t workspace_bytes() const {
+    return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + ws.bytes();
+  }
+};

@@ -1,0 +1,648 @@
+// capi_score.cpp -- C ABI of the generalized scoring path: fp32-query int4
+// scoring with reducers and candidates (CudaInt4PackedDocs.maxsim_batch /
+// topk_batch / score_*_batch, cu:2835-2991, score_impl cu:3124-3206), the
+// fused int4 residual (cu:2911-2955), and the binary corpus handle
+// CudaPackedDocs (cu:1872-2675).  Kernels: score.hip.
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "capi_handles.hpp"
+
+namespace msim {
+
+namespace {
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Upload host tables; returns the device pointers.
+template <typename T>
+T* upload_vec(DeviceBuffer& buf, const std::vector<T>& v, const char* what) {
+  buf.ensure(std::max<size_t>(sizeof(T) * v.size(), sizeof(T)), what);
+  if (!v.empty()) check_hip(hipMemcpy(buf.ptr, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice), what);
+  return buf.as<T>();
+}
+
+}  // namespace
+
+void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int64_t num_tokens,
+                       const DocStreams& s, const QueryInput& q, int reducer, float temperature,
+                       int64_t batch, int64_t query_tokens, const float* h_row_weights, const Targets& t,
+                       float* d_out, int64_t out_stride, int32_t* d_iout, hipStream_t stream) {
+  const int64_t num_docs = (int64_t)off.size() - 1;
+  const int64_t targets = t.host ? t.count : num_docs;
+  if (batch == 0 || targets == 0) return;
+  const int64_t rows = batch * query_tokens;
+  if (query_tokens == 0 || num_tokens == 0) {
+    // No query tokens, or every document is empty: every score is 0.
+    for (int64_t b = 0; b < batch; ++b)
+      if (d_out) check_hip(launch_fill_f32(d_out + b * out_stride, targets, 0.0f, stream), "zero scores");
+    // int32 zero has the bit pattern of 0.0f.
+    if (d_iout) check_hip(launch_fill_f32(reinterpret_cast<float*>(d_iout), batch * targets, 0.0f, stream), "zero scores");
+    return;
+  }
+  const int limbs = q.limbs;
+  const int64_t rows_padded = ceil_div(rows, 16) * 16 + 128;
+
+  // 1. Quantise the query rows.
+  ws.qpack.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs");
+  ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
+  ws.qsum.ensure(sizeof(int32_t) * limbs * rows_padded, "hipMalloc query limb sums");
+  if (q.d_qbits)
+    check_hip(launch_quantize_bits(q.d_qbits, rows, rows_padded, ws.qpack.as<int8_t>(), ws.colmul.as<float>(),
+                                   ws.qsum.as<int32_t>(), stream),
+              "launch sign query kernel");
+  else
+    check_hip(launch_quantize_limbs(q.d_query, rows, rows_padded, limbs, s.doc, q.recip, ws.qpack.as<int8_t>(),
+                                    ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream),
+              "launch query quantize kernel");
+
+  // 2. Reducer weights, one per query row (padding rows 0).
+  const float* d_weights = nullptr;
+  if (h_row_weights) {
+    std::vector<float> w((size_t)rows_padded, 0.0f);
+    std::memcpy(w.data(), h_row_weights, sizeof(float) * rows);
+    d_weights = upload_vec(ws.weights, w, "copy reducer query weights to device");
+  }
+
+  // 3. Work split.
+  const int64_t groups = t.per_row ? batch : 1;
+  const int64_t grp_rows = t.per_row ? query_tokens : rows;
+  const int64_t rpp = score_rows_per_pass(limbs, grp_rows);
+  const int64_t subs = ceil_div(grp_rows, rpp);
+  const int64_t per_target = t.per_row ? t.count : targets;
+  int64_t waves = ceil_div((int64_t)device_cu_count() * 8, groups * subs);
+  waves = std::max<int64_t>(1, std::min(waves, per_target));
+
+  ScoreArgs a{};
+  const int64_t* d_targets = nullptr;
+  if (!t.host) {
+    if (ws.full_key != waves) {
+      std::vector<int64_t> info;
+      std::vector<uint64_t> tiles;
+      build_score_tables(off.data(), nullptr, num_docs, waves, info, tiles);
+      upload_vec(ws.full_info, info, "copy score wave table to device");
+      upload_vec(ws.full_tiles, tiles, "copy score tile table to device");
+      ws.full_key = waves;
+      ws.full_waves = (int64_t)info.size() / kScoreInfoWords;
+    }
+    a.wave_info = ws.full_info.as<int64_t>();
+    a.tiles = ws.full_tiles.as<uint64_t>();
+    a.num_waves = ws.full_waves;
+    a.info_grp_stride = 0;
+  } else {
+    // Per group: its own table, all padded to the same wave count.
+    std::vector<std::vector<int64_t>> infos((size_t)groups);
+    std::vector<uint64_t> tiles;
+    int64_t max_waves = 0;
+    for (int64_t gi = 0; gi < groups; ++gi) {
+      std::vector<uint64_t> gt;
+      build_score_tables(off.data(), t.host + gi * (t.per_row ? t.count : 0), per_target, waves, infos[gi], gt);
+      for (size_t w = 0; w < infos[gi].size(); w += kScoreInfoWords) infos[gi][w + 3] += (int64_t)tiles.size();
+      tiles.insert(tiles.end(), gt.begin(), gt.end());
+      max_waves = std::max<int64_t>(max_waves, (int64_t)infos[gi].size() / kScoreInfoWords);
+    }
+    std::vector<int64_t> info;
+    for (int64_t gi = 0; gi < groups; ++gi) {
+      auto& gi_info = infos[gi];
+      while ((int64_t)gi_info.size() / kScoreInfoWords < max_waves) {
+        const int64_t pad[kScoreInfoWords] = {per_target, 0, 0, 0};
+        gi_info.insert(gi_info.end(), pad, pad + kScoreInfoWords);
+      }
+      info.insert(info.end(), gi_info.begin(), gi_info.end());
+    }
+    a.wave_info = upload_vec(ws.cand_info, info, "copy candidate wave table to device");
+    a.tiles = upload_vec(ws.cand_tiles, tiles, "copy candidate tile table to device");
+    a.num_waves = max_waves;
+    a.info_grp_stride = max_waves * kScoreInfoWords;
+    std::vector<int64_t> ids(t.host, t.host + groups * per_target);
+    d_targets = upload_vec(ws.cand_ids, ids, "copy candidates to device");
+  }
+
+  // 4. Score into pooled[target][row], then sum each batch row's query tokens.
+  ws.pooled.ensure(sizeof(float) * std::max<int64_t>(1, groups * per_target * grp_rows), "hipMalloc pooled rows");
+  a.codes = s.codes;
+  a.tscale = s.tscale;
+  a.tmul = s.tmul;
+  a.rcodes = s.rcodes;
+  a.rtscale = s.rtscale;
+  a.rmul = s.rmul;
+  a.targets = d_targets;
+  a.targets_grp_stride = t.per_row ? t.count : 0;
+  a.qpack = ws.qpack.as<int8_t>();
+  a.rows_padded = rows_padded;
+  a.colmul = ws.colmul.as<float>();
+  a.qsum = ws.qsum.as<int32_t>();
+  a.weights = d_weights;
+  a.subs = (int32_t)subs;
+  a.grp_rows = (int32_t)grp_rows;
+  a.doc_scale = s.doc_scale;
+  a.scale = s.scale;
+  a.temperature = temperature;
+  a.pooled = ws.pooled.as<float>();
+  a.pooled_grp_stride = per_target * grp_rows;
+  check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
+  const int64_t bs = t.per_row ? per_target * query_tokens : query_tokens;
+  const int64_t ts = t.per_row ? query_tokens : rows;
+  check_hip(launch_pool_sum(ws.pooled.as<float>(), batch, query_tokens, per_target, bs, ts, d_out, out_stride, d_iout,
+                            stream),
+            "launch pooled sum kernel");
+}
+
+}  // namespace msim
+
+using namespace msim;
+
+namespace {
+
+int parse_reducer(const char* name) {
+  const std::string r = name ? name : "";
+  if (r == "maxsim" || r == "weighted_maxsim") return kRedMax;
+  if (r == "topk2") return kRedTop2;
+  if (r == "topk4") return kRedTop4;
+  if (r == "smoothsim") return kRedLse;
+  throw InvalidArgument("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'");
+}
+
+// Per-row weights [batch * query_tokens] from the caller's [Q], [1, Q] or
+// [B, Q] array (upload_reducer_weights, cu:3080-3122).
+std::vector<float> row_weights(const char* reducer, const float* w, int64_t ndim, int64_t d0, int64_t d1,
+                               int64_t batch, int64_t query_tokens) {
+  const bool requires = std::string(reducer ? reducer : "") == "weighted_maxsim";
+  if (w == nullptr || ndim == 0) {
+    if (requires) throw InvalidArgument("query_weights are required for reducer='weighted_maxsim'");
+    return {};
+  }
+  if (!requires) throw InvalidArgument("query_weights are only valid for reducer='weighted_maxsim'");
+  bool batched = false;
+  if (ndim == 1 && d0 == query_tokens) {
+    batched = false;
+  } else if (ndim == 2 && d1 == query_tokens && (d0 == 1 || d0 == batch)) {
+    batched = d0 == batch;
+  } else {
+    throw InvalidArgument("query_weights must have shape [query_tokens] or [batch, query_tokens]");
+  }
+  std::vector<float> out((size_t)(batch * query_tokens));
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t q = 0; q < query_tokens; ++q) out[b * query_tokens + q] = w[(batched ? b * query_tokens : 0) + q];
+  return out;
+}
+
+void check_temperature(double t) {
+  if (!(t > 0.0) || !std::isfinite(t)) throw InvalidArgument("temperature must be finite and > 0");
+}
+
+void check_candidates(const int64_t* c, int64_t m, int64_t num_docs) {
+  if (m < 0) throw InvalidArgument("candidate_indices must be a 1-D array");
+  for (int64_t i = 0; i < m; ++i)
+    if (c[i] < 0 || c[i] >= num_docs)
+      throw InvalidArgument("candidate_indices entries must be between 0 and num_docs - 1");
+}
+
+void select_device(int device) { check_hip(hipSetDevice(device), "hipSetDevice"); }
+
+void check_k(int64_t k, int64_t n) {
+  if (k < 1 || k > n) throw InvalidArgument("k must be between 1 and num_docs");
+  if (k > kTopkMaxK) throw NotSupported("k above 4096 is not supported by the device top-k selector");
+}
+
+// fp32 query [B, Q, dim] (host) -> device [B * Q, 128], zero-padded dims.
+const float* upload_query128(ScoreWorkspace& ws, const float* query, int64_t rows, int64_t dim) {
+  const size_t bytes = sizeof(float) * (size_t)std::max<int64_t>(rows, 1) * 128;
+  ws.query.ensure(bytes, "hipMalloc query cache");
+  if (rows == 0) return ws.query.as<float>();
+  if (dim == 128) {
+    check_hip(hipMemcpy(ws.query.ptr, query, sizeof(float) * rows * 128, hipMemcpyHostToDevice), "copy query to device");
+  } else {
+    std::vector<float> wide((size_t)rows * 128, 0.0f);
+    for (int64_t r = 0; r < rows; ++r) std::memcpy(&wide[r * 128], query + r * dim, sizeof(float) * dim);
+    check_hip(hipMemcpy(ws.query.ptr, wide.data(), wide.size() * sizeof(float), hipMemcpyHostToDevice),
+              "copy query to device");
+  }
+  return ws.query.as<float>();
+}
+
+// ------------------------------------------------------------------ int4
+
+DocStreams int4_streams(msim_int4_docs* h, bool residual) {
+  if (h->dim > 128) throw NotSupported("fp32-query int4 scoring currently supports dim <= 128");
+  if (h->num_tokens > 0 && !h->has_token_scale && h->ones16.cap < (size_t)h->num_tokens * 4) {
+    std::vector<float> ones((size_t)h->num_tokens, 0.0625f);
+    h->ones16.ensure(ones.size() * 4, "hipMalloc int4 unit token scales");
+    check_hip(hipMemcpy(h->ones16.ptr, ones.data(), ones.size() * 4, hipMemcpyHostToDevice), "copy unit token scales");
+  }
+  DocStreams s;
+  s.doc = kDocInt4;
+  s.codes = h->dim < 128 ? h->codes128.as<uint8_t>() : h->packed.as<uint8_t>();
+  s.tscale = h->has_token_scale ? h->token_scales16.as<float>() : h->ones16.as<float>();
+  s.tmul = (float)h->scale;
+  s.scale = 1.0f;
+  if (residual) {
+    if (!h->has_residual)
+      throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
+    s.residual = true;
+    s.rcodes = h->dim < 128 ? h->residual128.as<uint8_t>() : h->residual_packed.as<uint8_t>();
+    s.rtscale = h->residual_token_scales16.as<float>();
+    s.rmul = (float)h->residual_scale;
+  }
+  return s;
+}
+
+void check_dim(int64_t dim, int64_t expected) {
+  if (dim != expected) throw InvalidArgument("query shape does not match dim");
+}
+
+// Scores of the fp32 query against every document (or candidates) into a
+// device buffer of [batch, targets]; returns it.
+float* int4_score_device(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens, int64_t dim,
+                         int reducer, const std::vector<float>& w, float temperature, const int64_t* cand,
+                         int64_t m, bool residual, hipStream_t stream) {
+  const int64_t targets = cand ? m : h->num_docs;
+  const DocStreams s = int4_streams(h, residual);
+  const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+  h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
+  QueryInput qi;
+  qi.d_query = d_query;
+  qi.limbs = 3;
+  Targets t{cand, m, false};
+  run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, reducer, temperature, batch, query_tokens,
+                    w.empty() ? nullptr : w.data(), t, h->scores.as<float>(), targets, nullptr, stream);
+  return h->scores.as<float>();
+}
+
+}  // namespace
+
+extern "C" int msim_int4_maxsim_batch(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                      int64_t dim, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    float* d = int4_score_device(h, query, batch, query_tokens, dim, kRedMax, {}, 1.0f, nullptr, 0, false, nullptr);
+    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+  });
+}
+
+extern "C" int msim_int4_topk_batch(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                    int64_t dim, int64_t k, float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    select_device(h->device);
+    float* d = int4_score_device(h, query, batch, query_tokens, dim, kRedMax, {}, 1.0f, nullptr, 0, false, nullptr);
+    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
+    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
+                          h->top_indices.as<int64_t>(), nullptr),
+              "launch topk selection kernel");
+    check_hip(hipMemcpy(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost),
+              "copy top scores to host");
+    check_hip(hipMemcpy(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost),
+              "copy top indices to host");
+  });
+}
+
+extern "C" int msim_int4_score(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                               int64_t dim, const char* reducer, const float* weights, int64_t weights_ndim,
+                               int64_t weights_dim0, int64_t weights_dim1, double temperature,
+                               const int64_t* candidates, int64_t num_candidates, int residual, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    if (candidates) check_candidates(candidates, num_candidates, h->num_docs);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    if (residual && !h->has_residual)
+      throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
+    const int64_t targets = candidates ? num_candidates : h->num_docs;
+    if (batch == 0 || targets == 0) return;
+    select_device(h->device);
+    float* d = int4_score_device(h, query, batch, query_tokens, dim, red, w, (float)temperature, candidates,
+                                 num_candidates, residual != 0, nullptr);
+    check_hip(hipMemcpy(out, d, sizeof(float) * batch * targets, hipMemcpyDeviceToHost), "copy output to host");
+  });
+}
+
+// ------------------------------------------------------------------ binary
+
+namespace {
+
+DocStreams binary_streams(msim_binary_docs* h, double scale, bool use_scale_vector, bool use_token_scale,
+                          const float* d_scale_override) {
+  if (use_scale_vector && !h->has_scale_vector)
+    throw InvalidArgument("scale vector was requested but is not loaded on this CUDA handle");
+  if (use_token_scale && !h->has_token_scale)
+    throw InvalidArgument("token scale vector was requested but is not loaded on this CUDA handle");
+  if (h->num_tokens > 0 && !(use_token_scale) && h->ones.cap < (size_t)h->num_tokens * 4) {
+    std::vector<float> ones((size_t)h->num_tokens, 1.0f);
+    h->ones.ensure(ones.size() * 4, "hipMalloc binary unit token scales");
+    check_hip(hipMemcpy(h->ones.ptr, ones.data(), ones.size() * 4, hipMemcpyHostToDevice), "copy unit token scales");
+  }
+  DocStreams s;
+  s.doc = kDocSign;
+  s.codes = h->packed.as<uint8_t>();
+  s.tscale = use_token_scale ? h->token_scales.as<float>() : h->ones.as<float>();
+  s.tmul = 1.0f;
+  s.doc_scale = d_scale_override ? d_scale_override : (use_scale_vector ? h->scale_vector.as<float>() : nullptr);
+  s.scale = (float)scale;
+  return s;
+}
+
+float* binary_score_device(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                           int64_t dim, int limbs, bool recip, const DocStreams& s, int reducer,
+                           const std::vector<float>& w, float temperature, const int64_t* cand, int64_t m) {
+  const int64_t targets = cand ? m : h->num_docs;
+  const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+  h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
+  QueryInput qi;
+  qi.d_query = d_query;
+  qi.limbs = limbs;
+  qi.recip = recip;
+  Targets t{cand, m, false};
+  run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, reducer, temperature, batch, query_tokens,
+                    w.empty() ? nullptr : w.data(), t, h->scores.as<float>(), targets, nullptr, nullptr);
+  return h->scores.as<float>();
+}
+
+void copy_topk_out(msim_binary_docs* h, const float* d_scores, int64_t batch, int64_t k, float* out_scores,
+                   int64_t* out_indices, hipStream_t stream) {
+  h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
+  h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+  check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
+                        h->top_indices.as<int64_t>(), stream),
+            "launch topk selection kernel");
+  check_hip(hipMemcpy(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost),
+            "copy top scores to host");
+  check_hip(hipMemcpy(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost),
+            "copy top indices to host");
+}
+
+void check_binary_query(const msim_binary_docs* h, int64_t batch, int64_t query_tokens, int64_t dim) {
+  require_shape(batch, query_tokens);
+  if (dim != h->dim) throw InvalidArgument("query shape does not match dim");
+}
+
+void check_int8q_dim(const msim_binary_docs* h) {
+  if (h->dim != 128) throw InvalidArgument("int8 query scoring currently requires dim=128");
+}
+
+}  // namespace
+
+extern "C" int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int64_t row_bytes,
+                                  const int64_t* offsets, int64_t num_offsets, int dim, msim_binary_docs** out) {
+  return guarded([&] {
+    if (out == nullptr) throw InvalidArgument("out handle pointer must not be NULL");
+    *out = nullptr;
+    if (dim <= 0 || dim % 8 != 0) throw InvalidArgument("dim must be positive and divisible by 8");
+    if (row_bytes != dim / 8) throw InvalidArgument("packed shape does not match dim");
+    if (dim > 128) throw NotSupported("binary scoring currently supports dim <= 128");
+    if (num_tokens < 0) throw InvalidArgument("packed must have shape [num_doc_tokens, dim / 8]");
+    validate_offsets(offsets, num_offsets, num_tokens);
+    if (num_tokens > 0 && packed == nullptr) throw InvalidArgument("packed must not be NULL");
+    auto h = std::make_unique<msim_binary_docs>();
+    check_hip(hipGetDevice(&h->device), "hipGetDevice");
+    h->dim = dim;
+    h->num_docs = num_offsets - 1;
+    h->num_tokens = num_tokens;
+    h->packed_size = (uint64_t)num_tokens * (uint64_t)row_bytes;
+    h->host_offsets.assign(offsets, offsets + num_offsets);
+    // Rows widened to 16 bytes: padding bits meet zero query dims.
+    std::vector<uint8_t> wide((size_t)std::max<int64_t>(num_tokens, 1) * 16, 0);
+    for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 16], packed + t * row_bytes, (size_t)row_bytes);
+    upload_vec(h->packed, wide, "copy binary packed docs to device");
+    std::vector<int64_t> offs(offsets, offsets + num_offsets);
+    upload_vec(h->offsets, offs, "copy binary offsets to device");
+    *out = h.release();
+  });
+}
+
+extern "C" int msim_binary_destroy(msim_binary_docs* h) {
+  return guarded([&] {
+    if (h == nullptr) return;
+    (void)hipSetDevice(h->device);
+    delete h;
+  });
+}
+
+extern "C" int msim_binary_set_scale_vector(msim_binary_docs* h, const float* scale, int64_t count) {
+  return guarded([&] {
+    require_handle(h);
+    if (count != h->num_docs) throw InvalidArgument("scale vector must have shape [num_docs]");
+    select_device(h->device);
+    std::vector<float> v(scale, scale + count);
+    upload_vec(h->scale_vector, v, "copy binary scale vector to device");
+    h->has_scale_vector = true;
+  });
+}
+
+extern "C" int msim_binary_clear_scale_vector(msim_binary_docs* h) {
+  return guarded([&] {
+    require_handle(h);
+    h->has_scale_vector = false;
+  });
+}
+
+extern "C" int msim_binary_set_token_scale(msim_binary_docs* h, const float* token_scales, int64_t count) {
+  return guarded([&] {
+    require_handle(h);
+    if (count != h->num_tokens) throw InvalidArgument("token scale vector must have shape [num_doc_tokens]");
+    select_device(h->device);
+    std::vector<float> v(token_scales, token_scales + count);
+    upload_vec(h->token_scales, v, "copy binary token scale vector to device");
+    h->has_token_scale = true;
+  });
+}
+
+extern "C" int msim_binary_clear_token_scale(msim_binary_docs* h) {
+  return guarded([&] {
+    require_handle(h);
+    h->has_token_scale = false;
+  });
+}
+
+extern "C" int msim_binary_get_props(const msim_binary_docs* h, msim_binary_props* out) {
+  return guarded([&] {
+    require_handle(h);
+    if (out == nullptr) throw InvalidArgument("props pointer must not be NULL");
+    out->dim = h->dim;
+    out->num_docs = h->num_docs;
+    out->num_tokens = h->num_tokens;
+    out->packed_size = h->packed_size;
+    out->has_scale_vector = h->has_scale_vector ? 1 : 0;
+    out->scale_vector_size = h->has_scale_vector ? (uint64_t)h->num_docs : 0;
+    out->has_token_scale_vector = h->has_token_scale ? 1 : 0;
+    out->token_scale_vector_size = h->has_token_scale ? (uint64_t)h->num_tokens : 0;
+    out->resident_bytes = h->resident_bytes();
+    out->workspace_bytes = h->workspace_bytes();
+  });
+}
+
+extern "C" int msim_binary_maxsim_batch(msim_binary_docs* h, const float* query, int64_t batch,
+                                        int64_t query_tokens, int64_t dim, double scale, int use_scale_vector,
+                                        int use_token_scale, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, kRedMax, {}, 1.0f, nullptr, 0);
+    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+  });
+}
+
+extern "C" int msim_binary_topk_batch(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                      int64_t dim, int64_t k, double scale, int use_scale_vector, int use_token_scale,
+                                      float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0) return;
+    select_device(h->device);
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, kRedMax, {}, 1.0f, nullptr, 0);
+    copy_topk_out(h, d, batch, k, out_scores, out_indices, nullptr);
+  });
+}
+
+extern "C" int msim_binary_maxsim_batch_int8q(msim_binary_docs* h, const float* query, int64_t batch,
+                                              int64_t query_tokens, int64_t dim, double scale, int use_scale_vector,
+                                              int use_token_scale, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_int8q_dim(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 1, true, s, kRedMax, {}, 1.0f, nullptr, 0);
+    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+  });
+}
+
+extern "C" int msim_binary_topk_batch_int8q(msim_binary_docs* h, const float* query, int64_t batch,
+                                            int64_t query_tokens, int64_t dim, int64_t k, double scale,
+                                            int use_scale_vector, int use_token_scale, float* out_scores,
+                                            int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_int8q_dim(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0) return;
+    select_device(h->device);
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 1, true, s, kRedMax, {}, 1.0f, nullptr, 0);
+    copy_topk_out(h, d, batch, k, out_scores, out_indices, nullptr);
+  });
+}
+
+extern "C" int msim_binary_score(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                 int64_t dim, const char* reducer, const float* weights, int64_t weights_ndim,
+                                 int64_t weights_dim0, int64_t weights_dim1, double temperature, double scale,
+                                 int use_scale_vector, int use_token_scale, const float* scale_vector_override,
+                                 const int64_t* candidates, int64_t num_candidates, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (candidates) check_candidates(candidates, num_candidates, h->num_docs);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    const int64_t targets = candidates ? num_candidates : h->num_docs;
+    if (batch == 0 || targets == 0) return;
+    select_device(h->device);
+    const float* d_override = nullptr;
+    if (scale_vector_override) {
+      std::vector<float> v(scale_vector_override, scale_vector_override + h->num_docs);
+      d_override = upload_vec(h->scale_override, v, "copy scale vector override to device");
+    }
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, d_override);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, red, w, (float)temperature,
+                                   candidates, num_candidates);
+    check_hip(hipMemcpy(out, d, sizeof(float) * batch * targets, hipMemcpyDeviceToHost), "copy output to host");
+  });
+}
+
+namespace {
+
+// Hamming MaxSim of sign-bit queries on the device: int32 [B, N] into
+// h->iscores and (when d_fscores) float scores.
+void hamming_device(msim_binary_docs* h, const uint8_t* d_qbits, int64_t batch, int64_t query_tokens,
+                    float* d_fscores, int32_t* d_iscores, hipStream_t stream) {
+  if (h->dim != 128) throw InvalidArgument("sign-query scoring currently requires dim=128");
+  DocStreams s = binary_streams(h, 1.0, false, false, nullptr);
+  QueryInput qi;
+  qi.d_qbits = d_qbits;
+  qi.limbs = 1;
+  Targets t{};
+  run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr, t,
+                    d_fscores, h->num_docs, d_iscores, stream);
+}
+
+const uint8_t* upload_qbits(msim_binary_docs* h, const uint8_t* qbits, int64_t rows) {
+  h->ws.qbits.ensure((size_t)std::max<int64_t>(rows, 1) * 16, "hipMalloc sign query cache");
+  if (rows) check_hip(hipMemcpy(h->ws.qbits.ptr, qbits, (size_t)rows * 16, hipMemcpyHostToDevice), "copy sign query");
+  return h->ws.qbits.as<uint8_t>();
+}
+
+}  // namespace
+
+extern "C" int msim_binary_hamming_batch(msim_binary_docs* h, const uint8_t* qbits, int64_t batch,
+                                         int64_t query_tokens, int64_t dim, int32_t* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    const uint8_t* d_q = upload_qbits(h, qbits, batch * query_tokens);
+    h->iscores.ensure(sizeof(int32_t) * batch * h->num_docs, "hipMalloc hamming scores");
+    hamming_device(h, d_q, batch, query_tokens, nullptr, h->iscores.as<int32_t>(), nullptr);
+    check_hip(hipMemcpy(out, h->iscores.ptr, sizeof(int32_t) * batch * h->num_docs, hipMemcpyDeviceToHost),
+              "copy hamming scores to host");
+  });
+}
+
+extern "C" int msim_binary_topk_hamming(msim_binary_docs* h, const uint8_t* qbits, int64_t batch,
+                                        int64_t query_tokens, int64_t dim, int64_t k, float* out_scores,
+                                        int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_binary_query(h, batch, query_tokens, dim);
+    if (batch == 0) return;
+    select_device(h->device);
+    const uint8_t* d_q = upload_qbits(h, qbits, batch * query_tokens);
+    h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
+    hamming_device(h, d_q, batch, query_tokens, h->scores.as<float>(), nullptr, nullptr);
+    copy_topk_out(h, h->scores.as<float>(), batch, k, out_scores, out_indices, nullptr);
+  });
+}
+
+extern "C" int msim_binary_topk_hamming_async(msim_binary_docs* h, const uint8_t* d_qbits, int64_t batch,
+                                              int64_t query_tokens, int64_t k, float* d_scores, int64_t* d_indices,
+                                              void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    select_device(h->device);
+    h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
+    hamming_device(h, d_qbits, batch, query_tokens, h->scores.as<float>(), nullptr, as_stream(stream));
+    check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr, d_scores, d_indices,
+                          as_stream(stream)),
+              "launch topk selection kernel");
+  });
+}

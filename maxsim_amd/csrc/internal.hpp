@@ -82,6 +82,58 @@ hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t
 void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves,
                        std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table);
 
+// Generalized scoring (score.hip): int4 or sign-bit documents, optional int4
+// residual stream, 1 (int8) or 3 (fp32 split into int8 limbs) query limbs,
+// reducers.  Targets are documents or candidate positions, walked from a
+// host-built table (build_score_tables): per wave kScoreInfoWords int64
+// words {first target, targets, tiles, first tile-table entry}, padded to
+// whole workgroups; per tile one entry: bits 0..39 first token, 40..43
+// rows - 1, 45 last tile of its target, 46 empty target (no tokens, token
+// 0 is read and masked), 48..63 target index relative to the wave's first;
+// one padding entry (token 0) follows every wave's tiles.
+constexpr int kScoreInfoWords = 4;
+enum : int { kDocInt4 = 0, kDocSign = 1 };
+enum : int { kRedMax = 0, kRedTop2 = 1, kRedTop4 = 2, kRedLse = 3 };
+struct ScoreArgs {
+  const uint8_t* codes;        // int4 [T, 64] or sign bits [T, 16]
+  const float* tscale;         // [T] per-token scale of `codes` (never null)
+  float tmul;                  // constant factor of the `codes` similarity
+  const uint8_t* rcodes;       // residual int4 codes [T, 64] (residual kernels)
+  const float* rtscale;        // [T] residual per-token scale
+  float rmul;
+  const int64_t* wave_info;    // [groups][num_waves][kScoreInfoWords]
+  const uint64_t* tiles;
+  int64_t num_waves;           // per group, a multiple of 4
+  int64_t info_grp_stride;     // int64 words between groups' wave tables (0 = shared)
+  const int64_t* targets;      // document of each target, or nullptr (target = document)
+  int64_t targets_grp_stride;  // entries between groups' target lists
+  const int8_t* qpack;         // [limbs][rows_padded][128] B-operand order
+  int64_t rows_padded;
+  const float* colmul;         // [rows_padded] per query row factor (sigma)
+  const int32_t* qsum;         // [limbs][rows_padded] limb sums (sign documents)
+  const float* weights;        // [rows_padded] weighted MaxSim factors or nullptr
+  int32_t subs;                // passes per group (query rows / rows per pass)
+  int32_t grp_rows;            // query rows per group
+  const float* doc_scale;      // [num_docs] per-document scale or nullptr
+  float scale;                 // document scale when doc_scale is null
+  float temperature;
+  float* pooled;               // pooled[g * pooled_grp_stride + target * grp_rows + row]
+  int64_t pooled_grp_stride;
+};
+int score_rows_per_pass(int limbs, int64_t rows);
+hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
+                        hipStream_t stream);
+hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
+                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream);
+hipError_t launch_quantize_bits(const uint8_t* d_qbits, int64_t rows, int64_t rows_padded, int8_t* qpack,
+                                float* colmul, int32_t* qsum, hipStream_t stream);
+hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tokens, int64_t targets, int64_t bs,
+                           int64_t ts, float* out, int64_t out_stride, int32_t* iout, hipStream_t stream);
+// Tables for `num_targets` targets (targets == nullptr: every document) split
+// over about `waves` waves, balanced by tiles + 1 per target.
+void build_score_tables(const int64_t* offsets, const int64_t* targets, int64_t num_targets, int64_t waves,
+                        std::vector<int64_t>& info, std::vector<uint64_t>& tiles);
+
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a
 // position to the reported id.

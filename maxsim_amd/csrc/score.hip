@@ -1,0 +1,509 @@
+// score.hip -- generalized MaxSim scoring on gfx950 MFMA: int4 or sign-bit
+// documents (optionally with an int4 residual stream), fp32 or int8 queries,
+// the reference's five reducers, full-corpus or candidate targets.
+//
+// Semantics restated from the reference:
+//  * reducers: MaxSim / weighted MaxSim / TopK2 / TopK4 / SmoothSim policies
+//    cu:477-653, CPU closed form _api.py:558-585; an empty document scores 0;
+//    the document scale is applied after the reduction except for SmoothSim,
+//    whose similarities are scaled first (cu:602-605);
+//  * int4 similarity s_t * scale * (q . v_t) (cu:1268-1323, K6 with the int4
+//    loader); residual fused similarity p s^p_t (q . v^p_t) + r s^r_t
+//    (q . v^r_t) reduced once (cu:967-1266, cascade.py:272-291);
+//  * sign documents: q . sign(d_t) times the token scale (cu:297-352), the
+//    int8-query form 2 (q8 . bits) - sum(q8) (cu:1368-1447).
+//
+// Design (MI355X): the dot products run on v_mfma_i32_16x16x64_i8.  An fp32
+// query row q is split into three int8 limbs on a common grid,
+//   q ~= sigma (a + b / 254 + c / 254^2),  sigma = max|q| / 127,
+// |a|, |b|, |c| <= 127, so q . v = sigma (A + B / 254 + C / 254^2) with exact
+// int32 limb dots A, B, C; the limb grid resolves q to 2^-24 of max|q|, as
+// fine as fp32 itself.  Three int8 MFMA passes cost less than one fp32 VALU
+// pass (int8 MFMA 5 POPS vs 157 TFLOP/s fp32).  An int8 query uses one limb.
+//
+// Work split: a wave owns a range of targets (documents, or candidate
+// positions) and walks their 16-token tiles from a host-built table; a tile
+// is the MFMA A operand (16 tokens x 128 dims), the query rows of the pass
+// are B operands held in registers.  Each lane keeps the reducer state of
+// its query column over its four token rows; at a target's last tile the
+// four lane groups are merged and the per-row pooled values are written to
+// pooled[target][row]; pool_sum_kernel then sums over each batch row's query
+// tokens.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace msim {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPerGroup = kThreads / kWave;
+constexpr float kLimbStep = 1.0f / 254.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLowest = -3.402823466e+38f;
+
+template <int RED>
+struct ReducerState;
+
+// kRedMax: running maximum.
+template <>
+struct ReducerState<kRedMax> {
+  float m;
+  __device__ void init() { m = kNegInf; }
+  __device__ void add4(const float (&z)[4], float) { m = fmaxf(fmaxf(m, fmaxf(z[0], z[1])), fmaxf(z[2], z[3])); }
+  __device__ void merge_xor(int mask, float) { m = fmaxf(m, __shfl_xor(m, mask)); }
+  __device__ float finish(int len, float colmul, float, float weight, float doc_scale) const {
+    return len == 0 ? 0.0f : m * colmul * weight * doc_scale;
+  }
+};
+
+// kRedTop2 / kRedTop4: the K largest values, sorted descending.
+template <int K>
+struct TopState {
+  float t[K];
+  __device__ void init() {
+#pragma unroll
+    for (int i = 0; i < K; ++i) t[i] = kNegInf;
+  }
+  __device__ void insert(float v) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const float hi = fmaxf(t[i], v);
+      v = fminf(t[i], v);
+      t[i] = hi;
+    }
+  }
+  __device__ void add4(const float (&z)[4], float) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) insert(z[r]);
+  }
+  __device__ void merge_xor(int mask, float) {
+    float o[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) o[i] = __shfl_xor(t[i], mask);
+#pragma unroll
+    for (int i = 0; i < K; ++i) insert(o[i]);
+  }
+  __device__ float finish(int len, float colmul, float, float, float doc_scale) const {
+    const int kept = len < K ? len : K;
+    if (kept == 0) return 0.0f;
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (i < kept) total += t[i];
+    return total / (float)kept * colmul * doc_scale;
+  }
+};
+template <>
+struct ReducerState<kRedTop2> : TopState<2> {};
+template <>
+struct ReducerState<kRedTop4> : TopState<4> {};
+
+// kRedLse: online log-sum-exp in base 2 over x = z * (colmul * doc_scale):
+// m = running maximum (starts at the lowest finite float so that masked
+// -inf values never form inf - inf), s = sum 2^((x - m) * log2(e) / tau).
+template <>
+struct ReducerState<kRedLse> {
+  float m, s, k;  // k = colmul * doc_scale of the current target
+  __device__ void init() {
+    m = kLowest;
+    s = 0.0f;
+  }
+  __device__ void add4(const float (&z)[4], float k2) {
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = z[r] * k;
+    const float mn = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+    float acc = s * exp2f((m - mn) * k2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc += exp2f((x[r] - mn) * k2);
+    s = acc;
+    m = mn;
+  }
+  __device__ void merge_xor(int mask, float k2) {
+    const float mo = __shfl_xor(m, mask), so = __shfl_xor(s, mask);
+    const float mn = fmaxf(m, mo);
+    s = s * exp2f((m - mn) * k2) + so * exp2f((mo - mn) * k2);
+    m = mn;
+  }
+  __device__ float finish(int len, float, float temperature, float, float) const {
+    return len == 0 ? 0.0f : m + temperature * logf(s);
+  }
+};
+
+// One tile of a stream, as loaded: lane (g, c) holds token c's bytes of lane
+// group g and the scales of token rows 4g .. 4g + 3.
+template <int DOC>
+struct TileCodes;
+template <>
+struct TileCodes<kDocInt4> {
+  v4u w;  // 16 bytes: dims 32g .. 32g + 31 as nibbles
+};
+template <>
+struct TileCodes<kDocSign> {
+  unsigned w;  // 32 sign bits: dims 32g .. 32g + 31
+};
+
+// A operands (two MFMAs of 64 dims) from the tile bytes.
+__device__ __forceinline__ void unpack_a(const TileCodes<kDocInt4>& t, v4i& a0, v4i& a1) {
+  // Nibbles moved to the high half of each byte: the int8 value is 16 v.
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    a0[x] = (int)((t.w[x] << 4) & 0xF0F0F0F0u);  // even dims
+    a1[x] = (int)(t.w[x] & 0xF0F0F0F0u);         // odd dims
+  }
+}
+__device__ __forceinline__ void unpack_a(const TileCodes<kDocSign>& t, v4i& a0, v4i& a1) {
+  // Dword i holds bits i, i + 8, i + 16, i + 24 as bytes 0/1 (dims 32g + 8j + i).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a0[i] = (int)((t.w >> i) & 0x01010101u);
+    a1[i] = (int)((t.w >> (i + 4)) & 0x01010101u);
+  }
+}
+
+template <int DOC, bool RES, int L, int NT, int RED>
+__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
+  const int lane = lane_id();
+  const int wave = wave_uniform(threadIdx.x / kWave);
+  const int g = lane >> 4, c = lane & 15;
+  const int grp = (int)blockIdx.y / p.subs, sub = (int)blockIdx.y % p.subs;
+  const int64_t gw = (int64_t)blockIdx.x * kWavesPerGroup + wave;
+  const auto info = as_constant(p.wave_info) + grp * p.info_grp_stride + gw * kScoreInfoWords;
+  const int64_t t0 = info[0];
+  const int ntiles = (int)info[2];
+  if (ntiles == 0) return;  // no barriers below: a wave may leave early
+  const auto tt = as_constant(p.tiles) + info[3];
+  const auto targets = p.targets ? as_constant(p.targets) + grp * p.targets_grp_stride : nullptr;
+  const auto doc_scale = p.doc_scale ? as_constant(p.doc_scale) : nullptr;
+  const int lr0 = sub * 16 * NT;                           // first local row of the pass
+  const int64_t grow0 = (int64_t)grp * p.grp_rows + lr0;  // its global query row
+
+  // Query B operands and per-column constants.
+  v4i bq[L][NT][2];
+  float colmul[NT], weight[NT];
+  int qsum[L][NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int64_t r = grow0 + 16 * j + c;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+      const v4i* src = reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + r) * 128 + 32 * g);
+      bq[l][j][0] = src[0];
+      bq[l][j][1] = src[1];
+      qsum[l][j] = DOC == kDocSign ? p.qsum[l * p.rows_padded + r] : 0;
+    }
+    colmul[j] = p.colmul[r];
+    weight[j] = p.weights ? p.weights[r] : 1.0f;
+  }
+  const float k2 = kLog2e / p.temperature;
+
+  ReducerState<RED> st[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) st[j].init();
+
+  struct Tile {
+    TileCodes<DOC> a;
+    TileCodes<kDocInt4> r;
+    float s[4], sr[4];
+  };
+  // Every load is unconditional: rows past a short document read its last
+  // token again (masked below); table padding entries point at token 0.
+  auto load = [&](uint64_t e, Tile& t) {
+    const int64_t start = (int64_t)(e & 0xFFFFFFFFFFull);
+    const int rows1 = (int)((e >> 40) & 15);
+    const int64_t tok = start + min(c, rows1);
+    if constexpr (DOC == kDocInt4)
+      t.a.w = *reinterpret_cast<const v4u*>(p.codes + tok * 64 + 16 * g);
+    else
+      t.a.w = *reinterpret_cast<const unsigned*>(p.codes + tok * 16 + 4 * g);
+    if constexpr (RES) t.r.w = *reinterpret_cast<const v4u*>(p.rcodes + tok * 64 + 16 * g);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int64_t tr = start + min(4 * g + rr, rows1);
+      t.s[rr] = p.tscale[tr];
+      if constexpr (RES) t.sr[rr] = p.rtscale[tr];
+    }
+  };
+
+  Tile cur, nxt;
+  uint64_t e = tt[0];
+  load(e, cur);
+  int len = 0;  // tokens of the current target seen so far (wave-uniform)
+  float dscale = 1.0f;
+  bool fresh = true;
+  for (int i = 0; i < ntiles; ++i) {
+    const uint64_t en = tt[i + 1];
+    load(en, nxt);
+    const int local = (int)(e >> 48);
+    const bool last = ((e >> 45) & 1) != 0;
+    const int rows = ((e >> 46) & 1) ? 0 : (int)((e >> 40) & 15) + 1;
+    if (fresh) {
+      const int64_t tg = t0 + local;
+      const int64_t doc = targets ? targets[tg] : tg;
+      dscale = doc_scale ? doc_scale[doc] : p.scale;
+      if constexpr (RED == kRedLse) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale;
+      }
+    }
+
+    v4i a0, a1;
+    unpack_a(cur.a, a0, a1);
+    v4i acc[L][NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int l = 0; l < L; ++l) {
+        acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], acc[l][j], 0, 0, 0);
+      }
+    v4i accr[RES ? L : 1][RES ? NT : 1];
+    if constexpr (RES) {
+      v4i r0, r1;
+      unpack_a(cur.r, r0, r1);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+          accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+          accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], accr[l][j], 0, 0, 0);
+        }
+    }
+
+    float srow[4], srrow[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      srow[rr] = cur.s[rr] * p.tmul;
+      srrow[rr] = RES ? cur.sr[rr] * p.rmul : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      float z[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        // Limb dots combined smallest first; sign documents recover the
+        // +-1 dot as 2 (q . bits) - sum(q).
+        float y[L];
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+          y[l] = DOC == kDocSign ? (float)(2 * acc[l][j][rr] - qsum[l][j]) : (float)acc[l][j][rr];
+        float Y = y[0];
+        if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
+        z[rr] = Y * srow[rr];
+        if constexpr (RES) {
+          float yr[L];
+#pragma unroll
+          for (int l = 0; l < L; ++l) yr[l] = (float)accr[l][j][rr];
+          float YR = yr[0];
+          if constexpr (L == 3) YR = fmaf(fmaf(yr[2], kLimbStep, yr[1]), kLimbStep, yr[0]);
+          z[rr] = z[rr] + YR * srrow[rr];
+        }
+      }
+      if (rows < 16) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          if (4 * g + rr >= rows) z[rr] = kNegInf;
+      }
+      st[j].add4(z, k2);
+    }
+    len += rows;
+
+    if (last) {
+      const int64_t tg = t0 + local;
+      float* out = p.pooled + grp * p.pooled_grp_stride + tg * p.grp_rows;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        st[j].merge_xor(16, k2);
+        st[j].merge_xor(32, k2);
+        const float v = st[j].finish(len, colmul[j], p.temperature, weight[j], dscale);
+        const int lr = lr0 + 16 * j + c;
+        if (g == 0 && lr < p.grp_rows) out[lr] = v;
+        st[j].init();
+      }
+      len = 0;
+    }
+    fresh = last;
+    cur = nxt;
+    e = en;
+  }
+}
+
+// ------------------------------------------------------------ quantisation
+
+// Byte position of dim d in a 128-byte query row for the MFMA B operands.
+// int4 documents: lane group g = d / 32 holds the even dims of its 32 in
+// bytes [32g, 32g + 16) and the odd dims in [32g + 16, 32g + 32) (the order
+// of the low / high nibbles).  Sign documents: byte 32g + 16 (i / 4) +
+// 4 (i % 4) + j holds dim 32g + 8j + i (the order of the unpacked bits).
+__device__ __forceinline__ int query_byte(int d, int layout) {
+  const int g = d >> 5, e = d & 31;
+  if (layout == kDocInt4) return 32 * g + (e & 1) * 16 + (e >> 1);
+  const int j = e >> 3, i = e & 7;
+  return 32 * g + 16 * (i >> 2) + 4 * (i & 3) + j;
+}
+
+// One wave per query row of 128 dims (lane l holds dims 2l, 2l + 1).
+// sigma = f32(max|q| / 127) (0 -> 1); limb l: a_l = clip(rint(r_l / s_l),
+// -127, 127), r_{l+1} = r_l - a_l s_l (one rounding), s_{l+1} = s_l / 254.
+// With `recip` (one limb) the quotient is q * (1 / sigma), the binary int8
+// query rounding of cu:1328-1366.  colmul = sigma; qsum[l] = sum of limb l.
+__global__ __launch_bounds__(256) void quantize_limbs_kernel(const float* __restrict__ query, int64_t rows,
+                                                             int64_t rows_padded, int limbs, int layout,
+                                                             int recip, int8_t* __restrict__ qpack,
+                                                             float* __restrict__ colmul,
+                                                             int32_t* __restrict__ qsum) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows_padded) return;
+  const int d0 = 2 * lane, d1 = 2 * lane + 1;
+  const int p0 = query_byte(d0, layout), p1 = query_byte(d1, layout);
+  if (row >= rows) {
+    for (int l = 0; l < limbs; ++l) {
+      int8_t* dst = qpack + (l * rows_padded + row) * 128;
+      dst[p0] = 0;
+      dst[p1] = 0;
+      if (lane == 0) qsum[l * rows_padded + row] = 0;
+    }
+    if (lane == 0) colmul[row] = 0.0f;
+    return;
+  }
+  const float2 v = reinterpret_cast<const float2*>(query + row * 128)[lane];
+  const float m = wave_reduce(fmaxf(fabsf(v.x), fabsf(v.y)), [](float x, float y) { return fmaxf(x, y); });
+  const float sigma = m == 0.0f ? 1.0f : __fdiv_rn(m, 127.0f);
+  float rx = v.x, ry = v.y, s = sigma;
+  for (int l = 0; l < limbs; ++l) {
+    float qx, qy;
+    if (recip) {
+      const float inv = __fdiv_rn(1.0f, s);
+      qx = rx * inv;
+      qy = ry * inv;
+    } else {
+      qx = __fdiv_rn(rx, s);
+      qy = __fdiv_rn(ry, s);
+    }
+    const int a = max(-127, min(127, (int)rintf(qx)));
+    const int b = max(-127, min(127, (int)rintf(qy)));
+    int8_t* dst = qpack + (l * rows_padded + row) * 128;
+    dst[p0] = (int8_t)a;
+    dst[p1] = (int8_t)b;
+    const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
+    if (lane == 0) qsum[l * rows_padded + row] = sum;
+    rx = fmaf(-(float)a, s, rx);
+    ry = fmaf(-(float)b, s, ry);
+    s = s * kLimbStep;
+  }
+  if (lane == 0) colmul[row] = sigma;
+}
+
+// Sign-binarised query rows (pack_signs bit order, 16 bytes per row) as
+// +-1 int8 codes in the sign-document layout; colmul = 1.
+__global__ __launch_bounds__(256) void quantize_bits_kernel(const uint8_t* __restrict__ qbits, int64_t rows,
+                                                            int64_t rows_padded, int8_t* __restrict__ qpack,
+                                                            float* __restrict__ colmul,
+                                                            int32_t* __restrict__ qsum) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= rows_padded) return;
+  const int d0 = 2 * lane, d1 = 2 * lane + 1;
+  int8_t* dst = qpack + row * 128;
+  int a = 0, b = 0;
+  if (row < rows) {
+    const unsigned byte = qbits[row * 16 + (d0 >> 3)];
+    a = ((byte >> (d0 & 7)) & 1) ? 1 : -1;
+    b = ((byte >> (d1 & 7)) & 1) ? 1 : -1;
+  }
+  dst[query_byte(d0, kDocSign)] = (int8_t)a;
+  dst[query_byte(d1, kDocSign)] = (int8_t)b;
+  const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
+  if (lane == 0) {
+    qsum[row] = sum;
+    colmul[row] = row < rows ? 1.0f : 0.0f;
+  }
+}
+
+// out[b, t] = sum over q < Q of pooled[b * bs + t * ts + q] (sequential, f32).
+__global__ __launch_bounds__(256) void pool_sum_kernel(const float* __restrict__ pooled, int64_t batch,
+                                                       int64_t query_tokens, int64_t targets, int64_t bs,
+                                                       int64_t ts, float* __restrict__ out, int64_t out_stride,
+                                                       int32_t* __restrict__ iout) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= batch * targets) return;
+  const int64_t b = idx / targets, t = idx % targets;
+  const float* src = pooled + b * bs + t * ts;
+  float sum = 0.0f;
+  for (int64_t q = 0; q < query_tokens; ++q) sum += src[q];
+  if (out) out[b * out_stride + t] = sum;
+  if (iout) iout[b * targets + t] = (int32_t)sum;
+}
+
+template <int DOC, bool RES, int L, int NT>
+hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s) {
+  switch (reducer) {
+    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse><<<grid, kThreads, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int score_rows_per_pass(int limbs, int64_t rows) {
+  // Three limbs keep at most four 16-row tiles of B operands in registers,
+  // one limb eight; small queries use two tiles.
+  const int max_nt = limbs == 3 ? 4 : 8;
+  return 16 * (rows <= 32 ? 2 : max_nt);
+}
+
+hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
+                        hipStream_t stream) {
+  if (a.num_waves <= 0 || a.num_waves % kWavesPerGroup != 0 || a.subs <= 0 || groups <= 0)
+    return hipErrorInvalidValue;
+  if (a.tscale == nullptr || (residual && (a.rcodes == nullptr || a.rtscale == nullptr)))
+    return hipErrorInvalidValue;
+  const int rpp = score_rows_per_pass(limbs, a.grp_rows);
+  const int nt = rpp / 16;
+  const dim3 grid((unsigned)(a.num_waves / kWavesPerGroup), (unsigned)(groups * a.subs));
+#define MSIM_SCORE_NT(DOC, RES, L)                                              \
+  return nt == 2 ? launch_red<DOC, RES, L, 2>(a, reducer, grid, stream)         \
+                 : launch_red<DOC, RES, L, (L == 3 ? 4 : 8)>(a, reducer, grid, stream)
+  if (doc == kDocInt4 && !residual && limbs == 3) { MSIM_SCORE_NT(kDocInt4, false, 3); }
+  if (doc == kDocInt4 && residual && limbs == 3) { MSIM_SCORE_NT(kDocInt4, true, 3); }
+  if (doc == kDocSign && !residual && limbs == 3) { MSIM_SCORE_NT(kDocSign, false, 3); }
+  if (doc == kDocSign && !residual && limbs == 1) { MSIM_SCORE_NT(kDocSign, false, 1); }
+  if (doc == kDocSign && residual && limbs == 1) { MSIM_SCORE_NT(kDocSign, true, 1); }
+#undef MSIM_SCORE_NT
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
+                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream) {
+  if (rows_padded <= 0) return hipSuccess;
+  const int64_t blocks = (rows_padded + 3) / 4;
+  quantize_limbs_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(d_query, rows, rows_padded, limbs, layout,
+                                                                        recip ? 1 : 0, qpack, colmul, qsum);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_bits(const uint8_t* d_qbits, int64_t rows, int64_t rows_padded, int8_t* qpack,
+                                float* colmul, int32_t* qsum, hipStream_t stream) {
+  if (rows_padded <= 0) return hipSuccess;
+  const int64_t blocks = (rows_padded + 3) / 4;
+  quantize_bits_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(d_qbits, rows, rows_padded, qpack, colmul,
+                                                                       qsum);
+  return hipGetLastError();
+}
+
+hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tokens, int64_t targets, int64_t bs,
+                           int64_t ts, float* out, int64_t out_stride, int32_t* iout, hipStream_t stream) {
+  const int64_t n = batch * targets;
+  if (n <= 0) return hipSuccess;
+  pool_sum_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(pooled, batch, query_tokens, targets,
+                                                                             bs, ts, out, out_stride, iout);
+  return hipGetLastError();
+}
+
+}  // namespace msim
