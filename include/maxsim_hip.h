@@ -141,6 +141,19 @@ int msim_int4_score(msim_int4_docs* h, const float* query, int64_t batch, int64_
                     int64_t weights_dim0, int64_t weights_dim1, double temperature,
                     const int64_t* candidates, int64_t num_candidates, int residual, float* out);
 
+/* cascade_topk(query, packed, k, candidates=M, reducer, query_weights,
+ * temperature) of a residual int4 corpus (cascade.py:294-393): prefix scores
+ * of every document, the top-M per batch row (score desc, id asc), fused
+ * prefix+residual scores of those M, top-k with ties by document id
+ * (cascade.py:436-453).  M == num_docs scores every document fused
+ * (cascade.py:342-351).  The reference selects and loops over batch rows on
+ * the host; here every stage stays on the device. */
+int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                           int64_t dim, int64_t k, int64_t candidates, const char* reducer,
+                           const float* weights, int64_t weights_ndim, int64_t weights_dim0,
+                           int64_t weights_dim1, double temperature, float* out_scores,
+                           int64_t* out_indices);
+
 /* ===================================================================== */
 /* Binary corpus handle: CudaPackedDocs (cuda_extension.cu:1872-2675).    */
 /* ===================================================================== */
@@ -214,6 +227,38 @@ int msim_binary_topk_hamming(msim_binary_docs* h, const uint8_t* qbits, int64_t 
 int msim_binary_topk_hamming_async(msim_binary_docs* h, const uint8_t* d_qbits, int64_t batch,
                                    int64_t query_tokens, int64_t k, float* d_scores,
                                    int64_t* d_indices, void* stream);
+
+/* ------------------------------------------------------------------- */
+/* Binary prefix + int4 residual format (no reference function: the     */
+/* reference ships int4 + int4 only, cascade.py:60-93).  Per token: sign  */
+/* bits (the handle's codes), prefix scale a_t = mean|x_t| (the handle's  */
+/* token scale vector) and a per-token int4 residual of x - a_t sign(x).  */
+/* Queries are quantised to int8 per row as in maxsim_batch_int8q of the  */
+/* int4 handle.  Coarse similarity a_t (q . sign_t); fused similarity     */
+/* a_t (q . sign_t) + s^r_t r (q . v^r_t); MaxSim reduction.              */
+/* ------------------------------------------------------------------- */
+/* Residual stream: u8 [T, 64] int4 codes, scale, f32 [T] token scales
+ * (as set_residual_int4 of the int4 handle, cu:2777-2831). */
+int msim_binary_set_residual(msim_binary_docs* h, const uint8_t* packed, int64_t num_tokens,
+                             int64_t row_bytes, double scale, const float* token_scales,
+                             int64_t count);
+int msim_binary_clear_residual(msim_binary_docs* h);
+/* Coarse (fused = 0) or fused (fused = 1) scores; candidates NULL (every
+ * document, out [B, N]) or i64 [B, num_candidates] per batch row (out
+ * [B, num_candidates]). */
+int msim_binary_binres_score(msim_binary_docs* h, const float* query, int64_t batch,
+                             int64_t query_tokens, int64_t dim, int fused, const int64_t* candidates,
+                             int64_t num_candidates, float* out);
+/* Coarse top-M -> fused rescoring -> top-k, on the device (the cascade of
+ * msim_int4_cascade_topk over this format). */
+int msim_binary_cascade_topk(msim_binary_docs* h, const float* query, int64_t batch,
+                             int64_t query_tokens, int64_t dim, int64_t k, int64_t candidates,
+                             float* out_scores, int64_t* out_indices);
+/* Device-resident form: d_query f32 [B, Q, 128], outputs [B, k]; enqueued on
+ * `stream`. */
+int msim_binary_cascade_topk_async(msim_binary_docs* h, const float* d_query, int64_t batch,
+                                   int64_t query_tokens, int64_t k, int64_t candidates,
+                                   float* d_scores, int64_t* d_indices, void* stream);
 
 #ifdef __cplusplus
 }

@@ -390,14 +390,15 @@ def topk_maxsim(query_tokens, packed: PackedDocs, k: int, *, scale=None, device=
     use_token_scale = isinstance(packed.token_scale, np.ndarray)
     if reducer_value == "maxsim" and not _scale_is_vector(resolved_scale):
         signs_only = (
-            np.issubdtype(query.dtype, np.integer)
+            packed.dim == 128
+            and np.issubdtype(query.dtype, np.integer)
             and not use_token_scale
             and float(resolved_scale) == 1.0
             and batches.shape[1] > 0
             and np.all(np.abs(query) == 1)
         )
         if signs_only:
-            scores, indices = resident.data.topk_hamming_batch(pack_query_signs(batches), int(k))
+            scores, indices = resident.data.topk_hamming(pack_query_signs(batches), int(k))
         else:
             scores, indices = resident.data.topk_batch(np.ascontiguousarray(batches, dtype=np.float32), int(k),
                                                        float(resolved_scale), False, use_token_scale)

@@ -178,6 +178,20 @@ class CudaInt4PackedDocs:
                                         query_weights=None, temperature=1.0):
         return self._score(query, candidate_indices, reducer, query_weights, temperature, True)
 
+    def cascade_topk(self, query, k, candidates, reducer="maxsim", query_weights=None, temperature=1.0):
+        """Prefix top-M -> fused residual rescoring -> top-k, all on the device
+        (the pipeline of cascade_topk, cascade.py:294-393)."""
+        q = _query3(query)
+        w, wnd, w0, w1 = _weights(query_weights)
+        k, m = int(k), int(candidates)
+        scores = np.empty((q.shape[0], max(k, 0)), np.float32)
+        indices = np.empty((q.shape[0], max(k, 0)), np.int64)
+        if not isinstance(reducer, str):
+            raise ValueError("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'")
+        check(self._lib.msim_int4_cascade_topk(self._h, ptr(q), *q.shape, k, m, reducer.encode(), ptr(w), wnd, w0,
+                                               w1, float(temperature), ptr(scores), ptr(indices)))
+        return scores, indices
+
     # ------------------------------------------------- device-resident (torch)
     def maxsim_int8q_async(self, query, out, stream=None):
         """Enqueue int8-query MaxSim on device tensors: query f32[B,Q,128] and
@@ -400,6 +414,49 @@ class CudaPackedDocs:
         b, q = int(qbits.shape[0]), int(qbits.shape[1])
         check(self._lib.msim_binary_topk_hamming_async(self._h, ptr(qbits), b, q, int(k), ptr(scores),
                                                        ptr(indices), _stream_ptr(stream)))
+
+    # ------------------------- binary prefix + int4 residual (this build)
+    def set_residual_int4(self, packed, scale, token_scales):
+        p = _u8(packed)
+        ts = _f32(token_scales)
+        if p.ndim != 2:
+            raise ValueError("residual packed data must have shape [num_doc_tokens, dim / 2]")
+        if ts.ndim != 1:
+            raise ValueError("residual token scale vector must have shape [num_doc_tokens]")
+        check(self._lib.msim_binary_set_residual(self._h, ptr(p), p.shape[0], p.shape[1], float(scale), ptr(ts),
+                                                 ts.shape[0]))
+
+    def clear_residual_int4(self):
+        check(self._lib.msim_binary_clear_residual(self._h))
+
+    def binres_score_batch(self, query, fused=True, candidate_indices=None):
+        """int8-query coarse (fused=False) or fused scores; candidate_indices
+        None or i64 [B, M] per batch row."""
+        q = _query3(query)
+        cand = None
+        if candidate_indices is not None:
+            cand = _i64(candidate_indices)
+            if cand.ndim != 2 or cand.shape[0] != q.shape[0]:
+                raise ValueError("candidate_indices must have shape [batch, candidates]")
+        targets = self.num_docs if cand is None else cand.shape[1]
+        out = np.empty((q.shape[0], targets), np.float32)
+        check(self._lib.msim_binary_binres_score(self._h, ptr(q), *q.shape, int(bool(fused)), ptr(cand),
+                                                 0 if cand is None else cand.shape[1], ptr(out)))
+        return out
+
+    def cascade_topk(self, query, k, candidates):
+        q = _query3(query)
+        k, m = int(k), int(candidates)
+        scores = np.empty((q.shape[0], max(k, 0)), np.float32)
+        indices = np.empty((q.shape[0], max(k, 0)), np.int64)
+        check(self._lib.msim_binary_cascade_topk(self._h, ptr(q), *q.shape, k, m, ptr(scores), ptr(indices)))
+        return scores, indices
+
+    def cascade_topk_async(self, query, k, candidates, scores, indices, stream=None):
+        """Enqueue on device tensors: query f32 [B, Q, 128], scores f32 [B, k], indices i64 [B, k]."""
+        b, q = int(query.shape[0]), int(query.shape[1])
+        check(self._lib.msim_binary_cascade_topk_async(self._h, ptr(query), b, q, int(k), int(candidates),
+                                                       ptr(scores), ptr(indices), _stream_ptr(stream)))
 
     # --------------------------------------------------------- properties
     def _props(self):

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, list] = {
     "msim_int4_topk_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_int4_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl,
                         c_vp, c_i64, c_int, c_vp],
+    "msim_int4_cascade_topk": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64,
+                               c_dbl, c_vp, c_vp],
     # binary handle
     "msim_binary_create": [c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_vp],
     "msim_binary_destroy": [c_vp],
@@ -62,6 +64,11 @@ SIGNATURES: dict[str, list] = {
     "msim_binary_hamming_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp],
     "msim_binary_topk_hamming": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_binary_topk_hamming_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "msim_binary_set_residual": [c_vp, c_vp, c_i64, c_i64, c_dbl, c_vp, c_i64],
+    "msim_binary_clear_residual": [c_vp],
+    "msim_binary_binres_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_vp],
+    "msim_binary_cascade_topk": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
+    "msim_binary_cascade_topk_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
 }
 
 _RESTYPES = {"msim_last_error": ctypes.c_char_p}

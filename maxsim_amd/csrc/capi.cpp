@@ -323,6 +323,8 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
     h->packed_size = (uint64_t)num_tokens * (uint64_t)row_bytes;
     h->offsets_size = (uint64_t)num_offsets;
     h->host_offsets.assign(offsets, offsets + num_offsets);
+    for (int64_t d = 0; d + 1 < num_offsets; ++d)
+      h->max_doc_tiles = std::max<int64_t>(h->max_doc_tiles, (offsets[d + 1] - offsets[d] + 15) / 16);
     h->packed.ensure(std::max<uint64_t>(h->packed_size, 64), "hipMalloc int4 packed docs");
     h->offsets.ensure(h->offsets_size * 8, "hipMalloc int4 offsets");
     if (h->packed_size)

@@ -16,9 +16,12 @@ struct ScoreWorkspace {
   int64_t full_key = -1;               // wave count the cached tables were built for
   int64_t full_waves = 0;              // waves in the cached table
   DeviceBuffer cand_ids, cand_info, cand_tiles;
+  // cascade: coarse scores, top-M candidates (scores / ids), fine scores
+  DeviceBuffer coarse, top_m_scores, top_m_ids, fine;
   uint64_t bytes() const {
     return qpack.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + query.cap + qbits.cap + full_info.cap +
-           full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap;
+           full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap + coarse.cap + top_m_scores.cap +
+           top_m_ids.cap + fine.cap;
   }
 };
 
@@ -28,6 +31,7 @@ struct QueryInput {
   const uint8_t* d_qbits = nullptr;  // sign bits [rows, 16] (pack_signs order)
   int limbs = 3;                     // 3: fp32 split into int8 limbs, 1: int8
   bool recip = false;                // int8 rounding q * (1 / sigma) (binary int8q)
+  bool quantized = false;            // the workspace already holds this query in this layout
 };
 
 // The document streams and scales of one scoring call.
@@ -50,6 +54,11 @@ struct Targets {
   const int64_t* host = nullptr;
   int64_t count = 0;
   bool per_row = false;
+  // Candidate lists already on the device ([batch][count], per_row): tables
+  // are written on the device; documents have at most max_doc_tiles tiles.
+  const int64_t* device = nullptr;
+  const int64_t* d_offsets = nullptr;
+  int64_t max_doc_tiles = 1;
 };
 
 // Scores of `batch` x `query_tokens` query rows against the targets into
@@ -73,6 +82,7 @@ struct msim_int4_docs {
   bool has_token_scale = false;
   bool has_residual = false;
   int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
+  int64_t max_doc_tiles = 1;    // 16-token tiles of the longest document
   std::vector<int64_t> host_offsets;
   int64_t partition_waves = 0;    // wave count the cached scan table was built for
   int64_t num_scan_waves = 0;     // rows of wave_info
@@ -106,11 +116,17 @@ struct msim_binary_docs {
   std::vector<int64_t> host_offsets;
   // codes padded to 16 bytes (128 dims) per token
   msim::DeviceBuffer packed, offsets, scale_vector, token_scales, ones, scale_override;
+  // int4 residual stream of the binary-prefix + int4-residual format
+  bool has_residual = false;
+  double residual_scale = 1.0;
+  int64_t max_doc_tiles = 1;  // 16-token tiles of the longest document
+  msim::DeviceBuffer residual_packed, residual_token_scales16;
   msim::DeviceBuffer scores, top_scores, top_indices, iscores;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
-    return packed.cap + offsets.cap + scale_vector.cap + token_scales.cap + ones.cap;
+    return packed.cap + offsets.cap + scale_vector.cap + token_scales.cap + ones.cap + residual_packed.cap +
+           residual_token_scales16.cap;
   }
   uint64_t workspace_bytes() const {
     return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + ws.bytes();

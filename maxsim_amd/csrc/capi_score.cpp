@@ -31,7 +31,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
                        int64_t batch, int64_t query_tokens, const float* h_row_weights, const Targets& t,
                        float* d_out, int64_t out_stride, int32_t* d_iout, hipStream_t stream) {
   const int64_t num_docs = (int64_t)off.size() - 1;
-  const int64_t targets = t.host ? t.count : num_docs;
+  const int64_t targets = (t.host || t.device) ? t.count : num_docs;
   if (batch == 0 || targets == 0) return;
   const int64_t rows = batch * query_tokens;
   if (query_tokens == 0 || num_tokens == 0) {
@@ -49,13 +49,17 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   ws.qpack.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs");
   ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
   ws.qsum.ensure(sizeof(int32_t) * limbs * rows_padded, "hipMalloc query limb sums");
-  if (q.d_qbits)
+  if (q.quantized) {
+    // reuse the workspace's quantised rows
+  } else if (q.d_qbits)
     check_hip(launch_quantize_bits(q.d_qbits, rows, rows_padded, ws.qpack.as<int8_t>(), ws.colmul.as<float>(),
                                    ws.qsum.as<int32_t>(), stream),
               "launch sign query kernel");
   else
-    check_hip(launch_quantize_limbs(q.d_query, rows, rows_padded, limbs, s.doc, q.recip, ws.qpack.as<int8_t>(),
-                                    ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream),
+    // A sign stream paired with an int4 residual is unpacked in the int4
+    // lane order, so both share the int4 query layout.
+    check_hip(launch_quantize_limbs(q.d_query, rows, rows_padded, limbs, s.residual ? kDocInt4 : s.doc, q.recip,
+                                    ws.qpack.as<int8_t>(), ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream),
               "launch query quantize kernel");
 
   // 2. Reducer weights, one per query row (padding rows 0).
@@ -77,7 +81,23 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
 
   ScoreArgs a{};
   const int64_t* d_targets = nullptr;
-  if (!t.host) {
+  if (t.device) {
+    // Candidate lists on the device: fixed-size target ranges per wave,
+    // tables written by candidate_tables_kernel.
+    const int64_t per_wave = ceil_div(per_target, waves);
+    const int64_t w4 = ceil_div(ceil_div(per_target, per_wave), 4) * 4;
+    const int64_t cap = per_wave * std::max<int64_t>(1, t.max_doc_tiles) + 1;
+    ws.cand_info.ensure(sizeof(int64_t) * groups * w4 * kScoreInfoWords, "hipMalloc candidate wave table");
+    ws.cand_tiles.ensure(sizeof(uint64_t) * groups * w4 * cap, "hipMalloc candidate tile table");
+    check_hip(launch_candidate_tables(t.device, per_target, groups, t.d_offsets, w4, per_wave, cap,
+                                      ws.cand_info.as<int64_t>(), ws.cand_tiles.as<uint64_t>(), stream),
+              "launch candidate table kernel");
+    a.wave_info = ws.cand_info.as<int64_t>();
+    a.tiles = ws.cand_tiles.as<uint64_t>();
+    a.num_waves = w4;
+    a.info_grp_stride = w4 * kScoreInfoWords;
+    d_targets = t.device;
+  } else if (!t.host) {
     if (ws.full_key != waves) {
       std::vector<int64_t> info;
       std::vector<uint64_t> tiles;
@@ -415,6 +435,8 @@ extern "C" int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int
     h->num_tokens = num_tokens;
     h->packed_size = (uint64_t)num_tokens * (uint64_t)row_bytes;
     h->host_offsets.assign(offsets, offsets + num_offsets);
+    for (int64_t d = 0; d + 1 < num_offsets; ++d)
+      h->max_doc_tiles = std::max<int64_t>(h->max_doc_tiles, (offsets[d + 1] - offsets[d] + 15) / 16);
     // Rows widened to 16 bytes: padding bits meet zero query dims.
     std::vector<uint8_t> wide((size_t)std::max<int64_t>(num_tokens, 1) * 16, 0);
     for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 16], packed + t * row_bytes, (size_t)row_bytes);
@@ -644,5 +666,251 @@ extern "C" int msim_binary_topk_hamming_async(msim_binary_docs* h, const uint8_t
     check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr, d_scores, d_indices,
                           as_stream(stream)),
               "launch topk selection kernel");
+  });
+}
+
+// ----------------------------------------------------------------- cascades
+
+namespace {
+
+void check_cascade(int64_t k, int64_t m, int64_t num_docs) {
+  if (k < 1 || k > m || m > num_docs)
+    throw InvalidArgument("cascade sizes must satisfy 1 <= k <= candidates <= num_docs");
+  if (m > kTopkMaxK || m > kSortMaxRow)
+    throw NotSupported("cascade candidate budgets above 4096 are not supported by the device selector");
+}
+
+// Coarse scores of every document -> the top-M candidates of each batch row
+// (score desc, document asc), put in document order -> fine scores of the
+// candidates -> top-k, ties by document id (cascade.py:294-453), all on the
+// device.  coarse(d_scores) and fine(d_candidate_ids, d_scores) enqueue the
+// two scoring passes.
+template <typename Coarse, typename Fine>
+void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t k, int64_t m, Coarse coarse,
+                    Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
+  ws.coarse.ensure(sizeof(float) * batch * num_docs, "hipMalloc cascade coarse scores");
+  coarse(ws.coarse.as<float>());
+  ws.top_m_scores.ensure(sizeof(float) * batch * m, "hipMalloc cascade candidate scores");
+  ws.top_m_ids.ensure(sizeof(int64_t) * batch * m, "hipMalloc cascade candidates");
+  check_hip(launch_topk(ws.coarse.as<float>(), batch, num_docs, num_docs, m, nullptr, ws.top_m_scores.as<float>(),
+                        ws.top_m_ids.as<int64_t>(), stream),
+            "launch cascade candidate selection");
+  check_hip(launch_sort_rows(ws.top_m_ids.as<int64_t>(), batch, m, stream), "launch candidate sort");
+  ws.fine.ensure(sizeof(float) * batch * m, "hipMalloc cascade fine scores");
+  fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>());
+  check_hip(launch_topk(ws.fine.as<float>(), batch, m, m, k, ws.top_m_ids.as<int64_t>(), d_top_s, d_top_i, stream),
+            "launch cascade final selection");
+}
+
+void copy_topk_host(const float* d_s, const int64_t* d_i, int64_t batch, int64_t k, float* out_s, int64_t* out_i) {
+  check_hip(hipMemcpy(out_s, d_s, sizeof(float) * batch * k, hipMemcpyDeviceToHost), "copy top scores to host");
+  check_hip(hipMemcpy(out_i, d_i, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost), "copy top indices to host");
+}
+
+}  // namespace
+
+extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                      int64_t dim, int64_t k, int64_t candidates, const char* reducer,
+                                      const float* weights, int64_t weights_ndim, int64_t weights_dim0,
+                                      int64_t weights_dim1, double temperature, float* out_scores,
+                                      int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    check_cascade(k, candidates, h->num_docs);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    if (!h->has_residual)
+      throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
+    if (batch == 0) return;
+    select_device(h->device);
+    const DocStreams prefix = int4_streams(h, false), fused = int4_streams(h, true);
+    QueryInput qi;
+    qi.d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+    qi.limbs = 3;
+    const float* wp = w.empty() ? nullptr : w.data();
+    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
+    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+    if (candidates == h->num_docs) {
+      // Every document is a candidate: full fused scoring (cascade.py:342-351).
+      h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
+      run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, red, (float)temperature, batch,
+                        query_tokens, wp, Targets{}, h->scores.as<float>(), h->num_docs, nullptr, nullptr);
+      check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr,
+                            h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr),
+                "launch topk selection kernel");
+    } else {
+      cascade_device(
+          h->ws, batch, h->num_docs, k, candidates,
+          [&](float* d) {
+            run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, qi, red, (float)temperature, batch,
+                              query_tokens, wp, Targets{}, d, h->num_docs, nullptr, nullptr);
+          },
+          [&](const int64_t* ids, float* d) {
+            Targets t;
+            t.device = ids;
+            t.count = candidates;
+            t.per_row = true;
+            t.d_offsets = h->offsets.as<int64_t>();
+            t.max_doc_tiles = h->max_doc_tiles;
+            QueryInput again = qi;
+            again.quantized = true;
+            run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, again, red, (float)temperature, batch,
+                              query_tokens, wp, t, d, candidates, nullptr, nullptr);
+          },
+          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr);
+    }
+    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+  });
+}
+
+// ------------------------------------- binary prefix + int4 residual format
+
+namespace {
+
+DocStreams binres_streams(msim_binary_docs* h, bool fused) {
+  if (h->dim != 128) throw InvalidArgument("binary residual scoring currently requires dim=128");
+  if (!h->has_token_scale)
+    throw InvalidArgument("binary residual scoring needs the prefix scales: call set_token_scale_vector first");
+  if (fused && !h->has_residual)
+    throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
+  DocStreams s;
+  s.doc = kDocSign;
+  s.codes = h->packed.as<uint8_t>();
+  s.tscale = h->token_scales.as<float>();
+  s.tmul = 1.0f;
+  if (fused) {
+    s.residual = true;
+    s.rcodes = h->residual_packed.as<uint8_t>();
+    s.rtscale = h->residual_token_scales16.as<float>();
+    s.rmul = (float)h->residual_scale;
+  }
+  return s;
+}
+
+void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, int64_t query_tokens, int64_t k,
+                    int64_t m, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
+  const DocStreams prefix = binres_streams(h, false), fused = binres_streams(h, true);
+  QueryInput qi;
+  qi.d_query = d_query;
+  qi.limbs = 1;
+  if (m == h->num_docs) {
+    h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
+    run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, kRedMax, 1.0f, batch, query_tokens, nullptr,
+                      Targets{}, h->scores.as<float>(), h->num_docs, nullptr, stream);
+    check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i,
+                          stream),
+              "launch topk selection kernel");
+    return;
+  }
+  cascade_device(
+      h->ws, batch, h->num_docs, k, m,
+      [&](float* d) {
+        run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, qi, kRedMax, 1.0f, batch, query_tokens,
+                          nullptr, Targets{}, d, h->num_docs, nullptr, stream);
+      },
+      [&](const int64_t* ids, float* d) {
+        // The fused pass reads its query in the int4 layout: quantised again.
+        Targets t;
+        t.device = ids;
+        t.count = m;
+        t.per_row = true;
+        t.d_offsets = h->offsets.as<int64_t>();
+        t.max_doc_tiles = h->max_doc_tiles;
+        run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, kRedMax, 1.0f, batch, query_tokens,
+                          nullptr, t, d, m, nullptr, stream);
+      },
+      d_top_s, d_top_i, stream);
+}
+
+}  // namespace
+
+extern "C" int msim_binary_set_residual(msim_binary_docs* h, const uint8_t* packed, int64_t num_tokens,
+                                        int64_t row_bytes, double scale, const float* token_scales, int64_t count) {
+  return guarded([&] {
+    require_handle(h);
+    if (h->dim != 128) throw InvalidArgument("binary residual data currently requires dim=128");
+    if (num_tokens != h->num_tokens || row_bytes != h->dim / 2)
+      throw InvalidArgument("residual packed data must have shape [num_doc_tokens, dim / 2]");
+    if (!(scale > 0.0) || !std::isfinite(scale)) throw InvalidArgument("residual scale must be finite and > 0");
+    if (count != h->num_tokens) throw InvalidArgument("residual token scale vector must have shape [num_doc_tokens]");
+    validate_positive_scales(token_scales, count, "residual token scales must be finite and > 0");
+    select_device(h->device);
+    std::vector<uint8_t> codes(packed, packed + (size_t)num_tokens * (size_t)row_bytes);
+    upload_vec(h->residual_packed, codes, "copy binary residual data to device");
+    std::vector<float> s16(token_scales, token_scales + count);
+    for (float& v : s16) v *= 0.0625f;
+    upload_vec(h->residual_token_scales16, s16, "copy binary residual token scales to device");
+    h->residual_scale = scale;
+    h->has_residual = true;
+  });
+}
+
+extern "C" int msim_binary_clear_residual(msim_binary_docs* h) {
+  return guarded([&] {
+    require_handle(h);
+    h->has_residual = false;
+  });
+}
+
+extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query, int64_t batch,
+                                        int64_t query_tokens, int64_t dim, int fused, const int64_t* candidates,
+                                        int64_t num_candidates, float* out) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    const DocStreams s = binres_streams(h, fused != 0);
+    if (candidates) {
+      if (num_candidates < 0) throw InvalidArgument("candidate_indices must have shape [batch, candidates]");
+      check_candidates(candidates, batch * num_candidates, h->num_docs);
+    }
+    const int64_t targets = candidates ? num_candidates : h->num_docs;
+    if (batch == 0 || targets == 0) return;
+    select_device(h->device);
+    QueryInput qi;
+    qi.d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+    qi.limbs = 1;
+    Targets t{candidates, num_candidates, candidates != nullptr};
+    h->scores.ensure(sizeof(float) * batch * targets, "hipMalloc score cache");
+    run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr, t,
+                      h->scores.as<float>(), targets, nullptr, nullptr);
+    check_hip(hipMemcpy(out, h->scores.ptr, sizeof(float) * batch * targets, hipMemcpyDeviceToHost),
+              "copy output to host");
+  });
+}
+
+extern "C" int msim_binary_cascade_topk(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                        int64_t dim, int64_t k, int64_t candidates, float* out_scores,
+                                        int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    check_cascade(k, candidates, h->num_docs);
+    binres_streams(h, true);
+    if (batch == 0) return;
+    select_device(h->device);
+    const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
+    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+    binres_cascade(h, d_query, batch, query_tokens, k, candidates, h->top_scores.as<float>(),
+                   h->top_indices.as<int64_t>(), nullptr);
+    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+  });
+}
+
+extern "C" int msim_binary_cascade_topk_async(msim_binary_docs* h, const float* d_query, int64_t batch,
+                                              int64_t query_tokens, int64_t k, int64_t candidates, float* d_scores,
+                                              int64_t* d_indices, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    require_shape(batch, query_tokens);
+    check_cascade(k, candidates, h->num_docs);
+    binres_streams(h, true);
+    if (batch == 0) return;
+    select_device(h->device);
+    binres_cascade(h, d_query, batch, query_tokens, k, candidates, d_scores, d_indices, as_stream(stream));
   });
 }

@@ -134,6 +134,16 @@ hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tok
 void build_score_tables(const int64_t* offsets, const int64_t* targets, int64_t num_targets, int64_t waves,
                         std::vector<int64_t>& info, std::vector<uint64_t>& tiles);
 
+// Cascade helpers (cascade.hip): tile tables of per-group candidate lists
+// written on the device (groups x waves waves of at most per_wave
+// candidates, cap table entries each), and an ascending sort of int64 rows
+// of at most kSortMaxRow values.
+constexpr int64_t kSortMaxRow = 4096;
+hipError_t launch_candidate_tables(const int64_t* d_cands, int64_t m, int64_t groups, const int64_t* d_offsets,
+                                   int64_t waves, int64_t per_wave, int64_t cap, int64_t* d_info,
+                                   uint64_t* d_tiles, hipStream_t stream);
+hipError_t launch_sort_rows(int64_t* d_rows, int64_t batch, int64_t n, hipStream_t stream);
+
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a
 // position to the reported id.

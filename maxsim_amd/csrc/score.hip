@@ -161,6 +161,19 @@ __device__ __forceinline__ void unpack_a(const TileCodes<kDocSign>& t, v4i& a0, 
     a1[i] = (int)((t.w >> (i + 4)) & 0x01010101u);
   }
 }
+// Sign bits in the int4 lane order (a0: even dims, a1: odd dims), for a sign
+// stream that shares its query operands with an int4 stream.  Bits 0, 2, 4, 6
+// of a byte move to bits 0, 8, 16, 24 by one multiply with 0x41041 (shifts
+// 0, 6, 12, 18): the partial products overlap only at bits 6, 12 and 18,
+// whose carries stop at bits 7, 13 and 19, away from the kept bits.
+__device__ __forceinline__ void unpack_a_int4_order(const TileCodes<kDocSign>& t, v4i& a0, v4i& a1) {
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const unsigned b = t.w >> (8 * x);
+    a0[x] = (int)(((b & 0x55u) * 0x41041u) & 0x01010101u);
+    a1[x] = (int)((((b >> 1) & 0x55u) * 0x41041u) & 0x01010101u);
+  }
+}
 
 template <int DOC, bool RES, int L, int NT, int RED>
 __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
@@ -249,7 +262,10 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
     }
 
     v4i a0, a1;
-    unpack_a(cur.a, a0, a1);
+    if constexpr (DOC == kDocSign && RES)
+      unpack_a_int4_order(cur.a, a0, a1);
+    else
+      unpack_a(cur.a, a0, a1);
     v4i acc[L][NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j)

@@ -1,0 +1,181 @@
+"""GPU parity of the cascades (int4 residual, binary prefix + int4 residual)
+and of the public API routes over the device handles."""
+import numpy as np
+import pytest
+
+from conftest import ragged_fixture
+
+pytestmark = pytest.mark.gpu
+
+REDUCERS = ("maxsim", "weighted_maxsim", "topk2", "topk4", "smoothsim")
+
+
+def _close(actual, expected, rtol=1e-5):
+    scale = max(1.0, float(np.max(np.abs(expected)))) if np.size(expected) else 1.0
+    np.testing.assert_allclose(actual, expected, rtol=rtol, atol=rtol * scale)
+
+
+def _stable(scores, k, tie_ids=None):
+    ids = np.arange(scores.shape[0]) if tie_ids is None else tie_ids
+    return np.lexsort((ids, -scores))[:k]
+
+
+def _corpus(n=300, seed=40, lo=1, hi=60):
+    from maxsim_amd import synthetic
+
+    c = synthetic.make_corpus(n, lo, hi, seed=seed)
+    return c.embeddings, c.offsets
+
+
+# ----------------------------------------------------------- int4 residual
+
+
+@pytest.mark.parametrize("reducer", REDUCERS)
+def test_int4_residual_cascade_equals_host_procedure(gpu, oracle, reducer):
+    """The device cascade returns what cascade.py:294-453 computes from the
+    same prefix and fused scores: coarse stable top-M, per-row rescoring,
+    final order by (fused score desc, document id asc)."""
+    from maxsim_amd import synthetic
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4, prefix_score, residual_int4_to_device, residual_score
+
+    docs, offsets = _corpus()
+    query = synthetic.make_queries(synthetic.make_corpus(300, 1, 60, seed=40), 3)
+    weights = np.random.default_rng(41).uniform(0.5, 1.5, size=(3, 32)).astype(np.float32)
+    w = weights if reducer == "weighted_maxsim" else None
+    packed = residual_int4_to_device(pack_residual_int4(docs, offsets))
+    k, m = 10, 64
+    top_s, top_i = cascade_topk(query, packed, k, candidates=m, reducer=reducer, query_weights=w, temperature=0.7)
+    coarse = prefix_score(query, packed, reducer=reducer, query_weights=w, temperature=0.7)
+    for b in range(3):
+        cands = _stable(coarse[b], m)
+        fine = residual_score(query[b], packed, reducer=reducer, query_weights=None if w is None else w[b],
+                              temperature=0.7, candidate_indices=cands)
+        order = _stable(fine, k, tie_ids=cands)
+        np.testing.assert_array_equal(top_i[b], cands[order])
+        np.testing.assert_array_equal(top_s[b], fine[order])
+    # and the fused scores are the oracle's
+    pcodes, pv, ps = oracle.pack_int4_token(docs)
+    prefix = pv.astype(np.float32) * ps[:, None]
+    _, rv, rs = oracle.pack_int4_token(docs - prefix)
+    recon = prefix + rv.astype(np.float32) * rs[:, None]
+    full = oracle.dense_scores(query, recon, offsets, reducer=reducer, weights=w, temperature=0.7)
+    _close(top_s, np.take_along_axis(full, top_i, axis=1))
+
+
+def test_int4_residual_cascade_full_budget_is_full_topk(gpu):
+    """candidates == num_docs gives the fused full top-k (tests/test_cascade.py:405-432)."""
+    from maxsim_amd import synthetic
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4, residual_int4_to_device, residual_score
+
+    docs, offsets = _corpus(120, 42)
+    query = synthetic.make_queries(synthetic.make_corpus(120, 1, 60, seed=42), 2)
+    packed = residual_int4_to_device(pack_residual_int4(docs, offsets))
+    s, i = cascade_topk(query, packed, 7, candidates=packed.num_docs)
+    full = residual_score(query, packed)
+    for b in range(2):
+        order = _stable(full[b], 7)
+        np.testing.assert_array_equal(i[b], order)
+        np.testing.assert_array_equal(s[b], full[b][order])
+
+
+def test_cascade_tie_order_by_document_id(gpu):
+    """Identical documents tie: the cascade keeps the lower ids (tests/test_cascade.py:389-402)."""
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4, residual_int4_to_device
+
+    rng = np.random.default_rng(43)
+    base = rng.standard_normal((4, 128)).astype(np.float32)
+    docs = np.concatenate([base] * 6)  # six identical 4-token documents
+    offsets = np.arange(0, 25, 4, dtype=np.int64)
+    packed = residual_int4_to_device(pack_residual_int4(docs, offsets))
+    _, idx = cascade_topk(rng.standard_normal((3, 128)).astype(np.float32), packed, 3, candidates=5)
+    np.testing.assert_array_equal(idx, [0, 1, 2])
+
+
+# --------------------------------------------------- binary prefix + residual
+
+
+def _binres(docs, offsets):
+    from maxsim_amd.binres import binres_to_device, pack_binary_residual
+
+    return binres_to_device(pack_binary_residual(docs, offsets))
+
+
+def test_binres_scores_match_oracle(gpu, oracle):
+    from maxsim_amd.binres import binres_score
+
+    docs, offsets = ragged_fixture(150, 44, lo=1, hi=50)
+    query = np.random.default_rng(45).standard_normal((3, 9, 128)).astype(np.float32)
+    packed = _binres(docs, offsets)
+    signs, a, _, rv, rs = oracle.pack_binary_residual(docs)
+    _close(binres_score(query, packed, fused=False), oracle.binres_prefix_scores(query, signs, a, offsets), 1e-6)
+    _close(binres_score(query, packed, fused=True),
+           oracle.binres_fused_scores(query, signs, a, rv, rs, offsets), 1e-6)
+    cand = np.random.default_rng(46).integers(0, 150, size=(3, 20)).astype(np.int64)
+    _close(binres_score(query, packed, fused=True, candidate_indices=cand),
+           oracle.binres_fused_scores(query, signs, a, rv, rs, offsets, candidates=cand), 1e-6)
+
+
+def test_binres_cascade_equals_host_procedure(gpu):
+    from maxsim_amd import synthetic
+    from maxsim_amd.binres import binres_cascade_topk, binres_score
+
+    corpus = synthetic.make_corpus(400, 64, 192, seed=47)
+    query = synthetic.make_queries(corpus, 4)
+    packed = _binres(corpus.embeddings, corpus.offsets)
+    k, m = 10, 128
+    top_s, top_i = binres_cascade_topk(query, packed, k, candidates=m)
+    coarse = binres_score(query, packed, fused=False)
+    cands = np.stack([_stable(coarse[b], m) for b in range(4)])
+    fine = binres_score(query, packed, fused=True, candidate_indices=cands)
+    for b in range(4):
+        order = _stable(fine[b], k, tie_ids=cands[b])
+        np.testing.assert_array_equal(top_i[b], cands[b][order])
+        np.testing.assert_array_equal(top_s[b], fine[b][order])
+    # the source document of each query is found
+    full = binres_score(query, packed, fused=True)
+    full_top = np.stack([_stable(full[b], k) for b in range(4)])
+    overlap = np.mean([len(set(top_i[b]) & set(full_top[b])) / k for b in range(4)])
+    assert overlap >= 0.9
+
+
+# ------------------------------------------------------------- public API
+
+
+def test_public_int4_routes(gpu, oracle):
+    import maxsim_amd as ms
+
+    docs, offsets = ragged_fixture(100, 48, lo=1, hi=30)
+    query = np.random.default_rng(49).standard_normal((2, 6, 128)).astype(np.float32)
+    packed = ms.pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    exp = oracle.int4_fp32_scores(query, packed.values, offsets, token_scale=packed.token_scale)
+    _close(ms.int4_maxsim(query, packed), exp)
+    _close(ms.score(query, packed, reducer="topk2"),
+           oracle.int4_fp32_scores(query, packed.values, offsets, token_scale=packed.token_scale, reducer="topk2"))
+    s, i = ms.topk_int4_maxsim(query, packed, 5, reducer="smoothsim", temperature=0.5)
+    full = ms.int4_maxsim(query, packed, reducer="smoothsim", temperature=0.5)
+    for b in range(2):
+        np.testing.assert_array_equal(i[b], _stable(full[b], 5))
+    s8, i8 = ms.topk_int4_maxsim(query, packed, 5, prefer_int8_query=True)
+    q8 = oracle.int4_int8q_scores(query, packed.values, offsets, token_scale=packed.token_scale)
+    np.testing.assert_array_equal(i8, oracle.topk(q8, 5)[1])
+
+
+def test_public_binary_routes(gpu, oracle):
+    import maxsim_amd as ms
+
+    docs, offsets = ragged_fixture(100, 50, lo=1, hi=30)
+    query = np.random.default_rng(51).standard_normal((2, 6, 128)).astype(np.float32)
+    packed = ms.pack_signs(docs, offsets, scale="doc", token_scale="mean_abs")
+    got = ms.maxsim(query, packed)
+    doc_of_token = np.repeat(np.arange(100), np.diff(offsets))
+    signs = np.where(docs >= 0, 1.0, -1.0).astype(np.float32)
+    recon = signs * (packed.token_scale * packed.scale[doc_of_token])[:, None]
+    _close(got, oracle.dense_scores(query, recon, offsets))
+    # +-1 integer queries take the sign-bit route; the result equals the float scoring
+    plain = ms.pack_signs(docs, offsets)
+    qi = np.where(query >= 0, 1, -1).astype(np.int8)
+    s, i = ms.topk_maxsim(qi, plain, 8)
+    full = ms.maxsim(qi.astype(np.float32), plain)
+    for b in range(2):
+        np.testing.assert_array_equal(i[b], _stable(full[b], 8))
+        _close(s[b], full[b][i[b]], 1e-6)

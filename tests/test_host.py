@@ -200,3 +200,41 @@ def test_config2_token_count():
     cfg = synthetic.CONFIGS[2]
     lengths = synthetic.doc_lengths(cfg["num_docs"], cfg["lo"], cfg["hi"])
     assert lengths.shape == (4096,) and int(lengths.sum()) == 523330
+
+
+def test_pack_binary_residual_matches_oracle(oracle):
+    from maxsim_amd.binres import pack_binary_residual
+
+    corpus = synthetic.make_corpus(40, 1, 30)
+    packed = pack_binary_residual(corpus.embeddings, corpus.offsets)
+    signs, a, rcodes, rvalues, rscale = oracle.pack_binary_residual(corpus.embeddings)
+    np.testing.assert_array_equal(packed.sign_data, signs)
+    np.testing.assert_array_equal(packed.prefix_scale, a)
+    np.testing.assert_array_equal(packed.residual_data, rcodes)
+    np.testing.assert_array_equal(packed.residual_values, rvalues)
+    np.testing.assert_array_equal(packed.residual_token_scale, rscale)
+    assert packed.storage_bytes == packed.num_tokens * 88
+
+
+def test_pack_residual_int4_two_stream_reconstruction():
+    """cascade.py:60-93: prefix = token int4 of x, residual = token int4 of x - prefix."""
+    from maxsim_amd.cascade import _reconstruct_int4, pack_residual_int4
+
+    corpus = synthetic.make_corpus(30, 1, 20)
+    packed = pack_residual_int4(corpus.embeddings, corpus.offsets)
+    prefix = _reconstruct_int4(packed.prefix_values, packed.prefix_scale, packed.prefix_token_scale)
+    res = pack_int4_symmetric(corpus.embeddings - prefix, corpus.offsets, scale_granularity="token")
+    np.testing.assert_array_equal(packed.residual_values, res.values)
+    recon = prefix + _reconstruct_int4(packed.residual_values, packed.residual_scale, packed.residual_token_scale)
+    assert np.max(np.abs(recon - corpus.embeddings)) < np.max(np.abs(prefix - corpus.embeddings))
+
+
+@pytest.mark.parametrize("kwargs,match", [({"candidates": 3, "k": 4}, "cascade sizes"),
+                                          ({"candidates": 99, "k": 1}, "cascade sizes")])
+def test_cascade_size_validation(kwargs, match):
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4
+
+    corpus = synthetic.make_corpus(10, 1, 5)
+    packed = pack_residual_int4(corpus.embeddings, corpus.offsets)
+    with pytest.raises(ValueError, match=match):
+        cascade_topk(np.ones((2, 128), np.float32), packed, kwargs["k"], candidates=kwargs["candidates"])
