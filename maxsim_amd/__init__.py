@@ -12,6 +12,16 @@ from maxsim_amd._api import (
     to_device,
     topk_maxsim,
 )
+from maxsim_amd.binres import BinaryResidualPackedDocs, binres_cascade_topk, binres_score, pack_binary_residual
+from maxsim_amd.cascade import (
+    ResidualInt4PackedDocs,
+    cascade_topk,
+    pack_residual_int4,
+    prefix_score,
+    prefix_topk,
+    residual_int4_to_device,
+    residual_score,
+)
 from maxsim_amd.experimental import (
     Int4PackedDocs,
     int4_maxsim,
@@ -21,7 +31,25 @@ from maxsim_amd.experimental import (
     topk_int4_maxsim,
 )
 
+from maxsim_amd.sdk import MODE_PRESETS, Corpus, Index, Reranker, SearchResult
+
 __all__ = [
+    "BinaryResidualPackedDocs",
+    "Corpus",
+    "Index",
+    "MODE_PRESETS",
+    "Reranker",
+    "ResidualInt4PackedDocs",
+    "SearchResult",
+    "binres_cascade_topk",
+    "binres_score",
+    "cascade_topk",
+    "pack_binary_residual",
+    "pack_residual_int4",
+    "prefix_score",
+    "prefix_topk",
+    "residual_int4_to_device",
+    "residual_score",
     "Int4PackedDocs",
     "PackedDocs",
     "int4_maxsim",

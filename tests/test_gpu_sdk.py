@@ -1,0 +1,104 @@
+"""Index / Reranker on the GPU: the reference's tests/test_sdk.py search and
+rerank expectations with device="cuda", and the config-2 route end to end."""
+import numpy as np
+import pytest
+
+import maxsim_amd as maxsim
+
+pytestmark = pytest.mark.gpu
+
+
+def _tiny():
+    docs = np.array([[1] * 8, [-1] * 8, [1, -1] * 4], dtype=np.float32)
+    return docs, np.array([0, 1, 2, 3], dtype=np.int64)
+
+
+def _reranker(mode, **kw):
+    docs, offsets = _tiny()
+    c = maxsim.Corpus.from_embeddings(["positive", "negative", "mixed"], docs, offsets, mode=mode)
+    return maxsim.Reranker.from_corpus(c, device="cuda", **kw)
+
+
+@pytest.mark.parametrize("mode", ["binary", "binary_token_scale", "int4", "int4_per_token", "int4_residual"])
+def test_search_single_and_batched(gpu, mode):
+    """tests/test_sdk.py:41-70."""
+    r = _reranker(mode)
+    res = r.search(np.ones((1, 8), np.float32), k=2)
+    assert [x.doc_id for x in res] == ["positive", "mixed"]
+    assert [x.rank for x in res] == [1, 2] and all(isinstance(x.score, float) for x in res)
+    q = np.array([[[1] * 8], [[-1] * 8]], np.float32)
+    out = r.search(q, k=1)
+    assert [[x.doc_id for x in row] for row in out] == [["positive"], ["negative"]]
+
+
+def test_rerank_candidates_and_unknown_id(gpu):
+    """tests/test_sdk.py:73-91."""
+    r = _reranker("binary")
+    res = r.rerank(np.ones((1, 8), np.float32), candidate_ids=["negative", "mixed", "mixed"], k=3)
+    assert [x.doc_id for x in res] == ["mixed", "negative"] and [x.rank for x in res] == [1, 2]
+    with pytest.raises(KeyError, match="missing"):
+        r.rerank(np.ones((1, 8), np.float32), candidate_ids=["missing"], k=1)
+
+
+def test_residual_mode_search_rerank_cascade(gpu):
+    """tests/test_sdk.py:214-246."""
+    from maxsim_amd.cascade import cascade_topk, residual_score
+
+    rng = np.random.default_rng(197)
+    lengths = np.array([2, 4, 1, 3, 5], np.int64)
+    offsets = np.concatenate(([0], np.cumsum(lengths))).astype(np.int64)
+    docs = rng.normal(size=(int(offsets[-1]), 8)).astype(np.float32)
+    query = rng.normal(size=(3, 8)).astype(np.float32)
+    ids = [f"doc-{i}" for i in range(5)]
+    corpus = maxsim.Index.from_embeddings(ids, docs, offsets, mode="int4_residual")
+    r = maxsim.Reranker.from_corpus(corpus, device="cuda")
+    cs, ci = cascade_topk(query, corpus.int4_packed, 2, candidates=4)
+    res = r.search(query, k=2, rescore_candidates=4)
+    assert [x.doc_id for x in res] == [ids[i] for i in ci]
+    np.testing.assert_allclose([x.score for x in res], cs, rtol=0, atol=1e-5)
+    reranked = r.rerank(query, ["doc-4", "doc-1", "doc-3"], k=3)
+    exp = residual_score(query, corpus.int4_packed, candidate_indices=np.array([4, 1, 3]))
+    order = np.lexsort((np.arange(3), -exp))
+    assert [x.doc_id for x in reranked] == [["doc-4", "doc-1", "doc-3"][i] for i in order]
+
+
+def test_rescore_candidates_requires_residual_mode(gpu):
+    with pytest.raises(ValueError, match="int4_residual"):
+        _reranker("int4_per_token").search(np.ones((1, 8), np.float32), k=2, rescore_candidates=3)
+
+
+def test_config2_route_int8_query_matches_oracle(gpu, oracle):
+    """Reranker(device='cuda', int4_query='int8').search on a per-token int4
+    index: ids and scores of the top-10 equal the C oracle's."""
+    from maxsim_amd import synthetic
+
+    corpus = synthetic.make_corpus(600, 64, 192, seed=7)
+    query = synthetic.make_queries(corpus, 4)
+    ids = [f"doc{i}" for i in range(600)]
+    index = maxsim.Index.from_embeddings(ids, corpus.embeddings, corpus.offsets, mode="int4_per_token")
+    r = maxsim.Reranker(index, device="cuda", int4_query="int8")
+    res = r.search(query, k=10)
+    p = index.int4_packed
+    exp = oracle.int4_int8q_scores(query, p.values, p.doc_offsets, token_scale=p.token_scale)
+    es, ei = oracle.topk(exp, 10)
+    assert [[x.doc_id for x in row] for row in res] == [[ids[i] for i in row] for row in ei]
+    assert [[x.score for x in row] for row in res] == es.astype(np.float64).tolist()
+
+
+def test_binary_residual_mode(gpu, oracle):
+    from maxsim_amd import synthetic
+
+    corpus = synthetic.make_corpus(300, 64, 192, seed=8)
+    query = synthetic.make_queries(corpus, 2)
+    ids = [f"d{i}" for i in range(300)]
+    index = maxsim.Index.from_embeddings(ids, corpus.embeddings, corpus.offsets, mode="binary_residual")
+    r = maxsim.Reranker(index, device="cuda")
+    full = r.search(query, k=5)
+    casc = r.search(query, k=5, rescore_candidates=300)
+    assert [[x.doc_id for x in row] for row in full] == [[x.doc_id for x in row] for row in casc]
+    signs, a, _, rv, rs = oracle.pack_binary_residual(corpus.embeddings)
+    exp = oracle.binres_fused_scores(query, signs, a, rv, rs, corpus.offsets)
+    for b in range(2):
+        got = np.array([x.score for x in full[b]])
+        idx = [ids.index(x.doc_id) for x in full[b]]
+        np.testing.assert_allclose(got, exp[b][idx], rtol=1e-6, atol=1e-5)
