@@ -55,6 +55,8 @@ def parse_args():
     ap.add_argument("--docs-per-wave", type=int, default=0)
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="append plain device copies of known size (PMC calibration)")
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                    help="BASELINE configuration to measure (2 = the headline metric)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print HBM traffic per scan launch from two rocprofv3 --pmc runs and exit")
     return ap.parse_args()
@@ -148,17 +150,7 @@ def cpu_baseline(packed, query, seconds: float):
     }
 
 
-def main():
-    args = parse_args()
-    if args.summarize_pmc:
-        print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
-        return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this build "
-              "scores on a single MI355X (the sharding design is written up in DESIGN.md)",
-              file=sys.stderr)
-        sys.exit(2)
-
+def bench_config2(args):
     import torch
 
     from maxsim_amd import _maxsim_hip, synthetic
@@ -329,6 +321,246 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+# ---------------------------------------------------------------- configs 3-5
+# Secondary measurements (the driver's line is config 2).  Each returns the
+# same JSON fields, with `config.workload` naming the configuration.
+
+MFMA_INT8_PEAK_TOPS = 5000.0
+FP32_PEAK_TFLOPS = 157.3
+
+
+def _timed(step, steps, warmup, stream):
+    """Wall ms per step over `steps` back-to-back steps, and per-step event ms."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = 1e3 * (time.perf_counter() - t0) / steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    return wall, np.array([a.elapsed_time(b) for a, b in ev])
+
+
+def _result(metric, value, unit, args, ms, p50, p95, dtype, workload, extra):
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": ms, "p50_ms": p50, "p95_ms": p95, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic (seeded normalised-Gaussian corpus, maxsim_amd/synthetic.py)",
+           "config": {"workload": workload}}
+    out.update(extra)
+    return out
+
+
+def bench_config3(args):
+    """fp32 query [4,32,128] x per-token int4 corpus (config-2 corpus), every
+    reducer in turn; one step = full scan + device top-10 for one reducer."""
+    import torch
+
+    from maxsim_amd import _maxsim_hip, synthetic
+    from maxsim_amd._native import check, ptr
+    from maxsim_amd.experimental import int4_to_device, pack_int4_symmetric
+
+    cfg = synthetic.CONFIGS[3]
+    corpus = synthetic.make_corpus(cfg["num_docs"], cfg["lo"], cfg["hi"])
+    query_np = synthetic.make_queries(corpus, cfg["batch"])
+    weights = np.random.default_rng(synthetic.SEED + 3).uniform(0.5, 1.5, size=query_np.shape[:2]).astype(np.float32)
+    packed = pack_int4_symmetric(corpus.embeddings, corpus.offsets, scale_granularity="token")
+    b, q = query_np.shape[:2]
+    n, t = packed.num_docs, int(packed.doc_offsets[-1])
+    torch.cuda.set_device(0)
+    h = int4_to_device(packed).data
+    lib = h._lib
+    stream = torch.cuda.current_stream()
+    sptr = _maxsim_hip._stream_ptr(stream)
+    dq = torch.from_numpy(query_np).cuda()
+    scores = torch.empty((b, n), dtype=torch.float32, device="cuda")
+    ts = torch.empty((b, args.k), dtype=torch.float32, device="cuda")
+    ti = torch.empty((b, args.k), dtype=torch.int64, device="cuda")
+    per = {}
+    for red in ("maxsim", "weighted_maxsim", "topk2", "topk4", "smoothsim"):
+        w = weights if red == "weighted_maxsim" else None
+        tau = 0.7 if red == "smoothsim" else 1.0
+
+        def step():
+            check(lib.msim_int4_score_async(h._h, ptr(dq), b, q, red.encode(), ptr(w), 0 if w is None else 2,
+                                            0 if w is None else b, 0 if w is None else q, tau, 0, ptr(scores), sptr))
+            check(lib.msim_topk_async(ptr(scores), b, n, n, args.k, ptr(ts), ptr(ti), sptr))
+
+        step()
+        torch.cuda.synchronize()
+        ref = h.score_batch(query_np, red, w, tau)
+        assert np.array_equal(scores.cpu().numpy(), ref), f"{red}: device-resident scores differ from the host API"
+        wall, ev = _timed(step, args.steps, args.warmup, stream)
+        per[red] = {"ms_per_step": wall, "p50_ms": float(np.percentile(ev, 50)), "docs_per_s": b * n / (wall * 1e-3)}
+    ms = float(np.mean([v["ms_per_step"] for v in per.values()]))
+    ops = 2.0 * b * q * t * 128  # multiply-adds x 2 of the fp32 contraction
+    roof = {"kernel": "score_kernel (3 int8 limbs)", "bound": "mfma", "unit": "TOP/s",
+            "achieved": 3 * ops / (ms * 1e-3) / 1e12, "peak": MFMA_INT8_PEAK_TOPS,
+            "fp32_equivalent_TFLOPs": ops / (ms * 1e-3) / 1e12, "fp32_vector_peak_TFLOPs": FP32_PEAK_TFLOPS,
+            "note": "step time (scan + top-10); int8 ops = 3 limbs x 2 B Q T 128"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+
+        orc.build()
+        sub = 512
+        start = time.perf_counter()
+        orc.int4_fp32_scores(query_np, packed.values, packed.doc_offsets[:sub + 1], token_scale=packed.token_scale)
+        el = time.perf_counter() - start
+        cpu = {"value": b * sub / el, "unit": "docs scored/s", "cores": 1, "kind": "port",
+               "sample": f"maxsim reducer, first {sub} docs x [4,32,128] fp32 query, C oracle, 1 thread, {el:.1f} s"}
+    return _result("docs scored/sec per reducer, int4 x fp32 query full scan + top-10 (1 GPU)", b * n / (ms * 1e-3),
+                   "docs scored/s", args, ms, float(np.mean([v["p50_ms"] for v in per.values()])), None, "f32",
+                   "BASELINE config 3: config-2 corpus, fp32 query [4,32,128], reducers maxsim / weighted (U[0.5,1.5]) "
+                   "/ topk2 / topk4 / smoothsim (tau 0.7), top-10",
+                   {"per_reducer": per, "roofline": roof, "cpu_baseline": cpu})
+
+
+def bench_config4(args):
+    """256 sign-binarised queries x 32 tokens over 10,240 binary documents of
+    256-1024 tokens; one step = all 256 queries + device top-10."""
+    import torch
+
+    from maxsim_amd import _maxsim_hip, synthetic
+    from maxsim_amd._api import pack_query_signs
+
+    cfg = synthetic.CONFIGS[4]
+    lengths = synthetic.doc_lengths(cfg["num_docs"], cfg["lo"], cfg["hi"])
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    codes = np.empty((int(offsets[-1]), 16), np.uint8)
+    first_tokens = []
+    for first, lens, emb in synthetic.iter_blocks(cfg["num_docs"], cfg["lo"], cfg["hi"]):
+        s0 = int(offsets[first])
+        bits = (emb >= 0).reshape(emb.shape[0], 16, 8).astype(np.uint8)
+        codes[s0:s0 + emb.shape[0]] = (bits << np.arange(8, dtype=np.uint8)).sum(axis=2, dtype=np.uint8)
+        if len(first_tokens) < cfg["batch"]:
+            first_tokens.append((first, lens, emb))
+    rng = np.random.default_rng(synthetic.SEED + 4)
+    # Queries: 32 noisy tokens of a document of the first block (the generator's recipe).
+    f, lens, emb = first_tokens[0]
+    loc = np.concatenate([[0], np.cumsum(lens)])
+    query = np.empty((cfg["batch"], 32, 128), np.float32)
+    for i in range(cfg["batch"]):
+        d = int(rng.integers(0, len(lens)))
+        tok = emb[loc[d]:loc[d + 1]][rng.choice(int(lens[d]), 32, replace=lens[d] < 32)]
+        query[i] = tok + rng.standard_normal(tok.shape).astype(np.float32) * np.float32(0.1)
+    qbits = pack_query_signs(query)
+    b, q, n, t = cfg["batch"], 32, cfg["num_docs"], int(offsets[-1])
+    torch.cuda.set_device(0)
+    h = _maxsim_hip.CudaPackedDocs(codes, offsets, 128)
+    stream = torch.cuda.current_stream()
+    dq = torch.from_numpy(qbits).cuda()
+    ts = torch.empty((b, args.k), dtype=torch.float32, device="cuda")
+    ti = torch.empty((b, args.k), dtype=torch.int64, device="cuda")
+
+    def step():
+        h.topk_hamming_async(dq, args.k, ts, ti, stream)
+
+    step()
+    torch.cuda.synchronize()
+    ref = h.hamming_batch(qbits[:8])
+    ref_ids = np.stack([np.lexsort((np.arange(n), -row))[:args.k] for row in ref])
+    assert np.array_equal(ti.cpu().numpy()[:8], ref_ids), "device top-k disagrees with device scores"
+    wall, ev = _timed(step, max(3, args.steps // 20), max(1, args.warmup // 10), stream)
+    ops = 2.0 * b * q * t * 128
+    roof = {"kernel": "score_kernel (sign docs, +-1 query)", "bound": "mfma", "unit": "TOP/s",
+            "achieved": ops / (wall * 1e-3) / 1e12, "peak": MFMA_INT8_PEAK_TOPS,
+            "note": "step time (scan of 8,192 query rows + top-10); ops = 2 B Q T 128 int8"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+
+        ref_ext = orc.reference_cpu_extension()
+        qs = np.where(query[0] >= 0, 1.0, -1.0).astype(np.float32)
+        start = time.perf_counter()
+        if ref_ext is not None:
+            ref_ext.maxsim_lut(qs, codes, offsets, 128, 1.0)
+            kind, src = "reference", "the reference's cpu_extension.cpp maxsim_lut (oracle/_ref)"
+        else:
+            orc.binary_lut_maxsim(qs, codes, offsets, 128)
+            kind, src = "port", "C oracle binary LUT"
+        el = time.perf_counter() - start
+        cpu = {"value": n / el, "unit": "docs scored/s", "cores": 1, "kind": kind,
+               "sample": f"1 of the 256 queries (32 tokens) x all {n} docs, {src}, 1 thread, {el:.1f} s"}
+    return _result("docs scored/sec, binary sign-query XOR/popcount-equivalent full scan + top-10 (1 GPU)",
+                   b * n / (wall * 1e-3), "docs scored/s", args, wall, float(np.percentile(ev, 50)),
+                   float(np.percentile(ev, 95)), "int8",
+                   f"BASELINE config 4: {n} binary docs x U{{256..1024}} tokens ({t} tokens), 256 x 32 sign queries, "
+                   "top-10",
+                   {"roofline": roof, "cpu_baseline": cpu})
+
+
+def bench_config5(args):
+    """Binary prefix + int4 residual corpus (config-2 documents), query
+    [4,32,128]: coarse scan -> top-512 -> fused rescoring -> top-10."""
+    import torch
+
+    from maxsim_amd import synthetic
+    from maxsim_amd.binres import binres_to_device, pack_binary_residual
+
+    cfg = synthetic.CONFIGS[5]
+    corpus = synthetic.make_corpus(cfg["num_docs"], cfg["lo"], cfg["hi"])
+    query_np = synthetic.make_queries(corpus, cfg["batch"])
+    packed = binres_to_device(pack_binary_residual(corpus.embeddings, corpus.offsets))
+    h = packed.sign_data
+    b, q, n, t = cfg["batch"], 32, cfg["num_docs"], int(corpus.offsets[-1])
+    stream = torch.cuda.current_stream()
+    dq = torch.from_numpy(query_np).cuda()
+    ts = torch.empty((b, args.k), dtype=torch.float32, device="cuda")
+    ti = torch.empty((b, args.k), dtype=torch.int64, device="cuda")
+    fs = torch.empty((b, args.k), dtype=torch.float32, device="cuda")
+    fi = torch.empty((b, args.k), dtype=torch.int64, device="cuda")
+
+    def step():
+        h.cascade_topk_async(dq, args.k, 512, ts, ti, stream)
+
+    def full():
+        h.cascade_topk_async(dq, args.k, n, fs, fi, stream)
+
+    wall, ev = _timed(step, args.steps, args.warmup, stream)
+    full_wall, _ = _timed(full, args.steps, args.warmup, stream)
+    got, exp = ti.cpu().numpy(), fi.cpu().numpy()
+    overlap = float(np.mean([len(set(got[i]) & set(exp[i])) / args.k for i in range(b)]))
+    return _result("docs scored/sec, binary-prefix top-512 -> fused int4-residual rescoring -> top-10 (1 GPU)",
+                   b * n / (wall * 1e-3), "docs scored/s", args, wall, float(np.percentile(ev, 50)),
+                   float(np.percentile(ev, 95)), "int8",
+                   f"BASELINE config 5: {n} docs ({t} tokens) as 16 B signs + 4 B prefix scale + 64 B int4 residual + "
+                   "4 B residual scale per token, query [4,32,128] int8, 512 candidates, top-10",
+                   {"full_fused_scan_ms_per_step": full_wall, "top10_overlap_vs_full_fused_scan": overlap,
+                    "bytes_per_token": 88, "cpu_baseline": None})
+
+
+OTHER_CONFIGS = {3: bench_config3, 4: bench_config4, 5: bench_config5}
+
+
+def main():
+    args = parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this build "
+              "scores on a single MI355X (the sharding design is written up in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.config == 2:
+        bench_config2(args)
+    else:
+        print(json.dumps(OTHER_CONFIGS[args.config](args)), flush=True)
 
 
 if __name__ == "__main__":

@@ -141,6 +141,15 @@ int msim_int4_score(msim_int4_docs* h, const float* query, int64_t batch, int64_
                     int64_t weights_dim0, int64_t weights_dim1, double temperature,
                     const int64_t* candidates, int64_t num_candidates, int residual, float* out);
 
+/* Device-resident form of msim_int4_score over every document (dim 128):
+ * d_query f32 [B, Q, 128] and d_out f32 [B, N] on the device; weights as
+ * msim_int4_score (host memory, read during the call); enqueued on
+ * `stream`. */
+int msim_int4_score_async(msim_int4_docs* h, const float* d_query, int64_t batch,
+                          int64_t query_tokens, const char* reducer, const float* weights,
+                          int64_t weights_ndim, int64_t weights_dim0, int64_t weights_dim1,
+                          double temperature, int residual, float* d_out, void* stream);
+
 /* cascade_topk(query, packed, k, candidates=M, reducer, query_weights,
  * temperature) of a residual int4 corpus (cascade.py:294-393): prefix scores
  * of every document, the top-M per batch row (score desc, id asc), fused

@@ -46,6 +46,7 @@ struct DocStreams {
   float rmul = 1.0f;
   const float* doc_scale = nullptr;
   float scale = 1.0f;
+  bool unit_tscale = false;  // tscale is all ones
 };
 
 // Candidate targets: none (every document), one list shared by all batch

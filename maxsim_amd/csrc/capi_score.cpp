@@ -140,8 +140,8 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
     d_targets = upload_vec(ws.cand_ids, ids, "copy candidates to device");
   }
 
-  // 4. Score into pooled[target][row], then sum each batch row's query tokens.
-  ws.pooled.ensure(sizeof(float) * std::max<int64_t>(1, groups * per_target * grp_rows), "hipMalloc pooled rows");
+  // 4. Score; the batch-row sums over query tokens are taken in the kernel
+  // or by pool_sum_kernel over pooled[target][row].
   a.codes = s.codes;
   a.tscale = s.tscale;
   a.tmul = s.tmul;
@@ -160,6 +160,19 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   a.doc_scale = s.doc_scale;
   a.scale = s.scale;
   a.temperature = temperature;
+  a.unit_tscale = s.unit_tscale;
+  a.query_tokens = (int32_t)query_tokens;
+  // Passes that hold whole batch rows let the kernel sum them itself.
+  const bool in_kernel_sum = t.per_row ? subs == 1 : rpp % query_tokens == 0;
+  if (in_kernel_sum) {
+    a.out = d_out;
+    a.out_stride = out_stride;
+    a.iout = d_iout;
+    a.iout_stride = per_target;
+    check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
+    return;
+  }
+  ws.pooled.ensure(sizeof(float) * std::max<int64_t>(1, groups * per_target * grp_rows), "hipMalloc pooled rows");
   a.pooled = ws.pooled.as<float>();
   a.pooled_grp_stride = per_target * grp_rows;
   check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
@@ -374,6 +387,7 @@ DocStreams binary_streams(msim_binary_docs* h, double scale, bool use_scale_vect
   s.tmul = 1.0f;
   s.doc_scale = d_scale_override ? d_scale_override : (use_scale_vector ? h->scale_vector.as<float>() : nullptr);
   s.scale = (float)scale;
+  s.unit_tscale = !use_token_scale;
   return s;
 }
 
@@ -690,12 +704,18 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
                     Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   ws.coarse.ensure(sizeof(float) * batch * num_docs, "hipMalloc cascade coarse scores");
   coarse(ws.coarse.as<float>());
-  ws.top_m_scores.ensure(sizeof(float) * batch * m, "hipMalloc cascade candidate scores");
   ws.top_m_ids.ensure(sizeof(int64_t) * batch * m, "hipMalloc cascade candidates");
-  check_hip(launch_topk(ws.coarse.as<float>(), batch, num_docs, num_docs, m, nullptr, ws.top_m_scores.as<float>(),
-                        ws.top_m_ids.as<int64_t>(), stream),
-            "launch cascade candidate selection");
-  check_hip(launch_sort_rows(ws.top_m_ids.as<int64_t>(), batch, m, stream), "launch candidate sort");
+  if (num_docs <= kSortMaxRow) {
+    check_hip(launch_select_topm(ws.coarse.as<float>(), batch, num_docs, num_docs, m, ws.top_m_ids.as<int64_t>(),
+                                 stream),
+              "launch cascade candidate selection");
+  } else {
+    ws.top_m_scores.ensure(sizeof(float) * batch * m, "hipMalloc cascade candidate scores");
+    check_hip(launch_topk(ws.coarse.as<float>(), batch, num_docs, num_docs, m, nullptr, ws.top_m_scores.as<float>(),
+                          ws.top_m_ids.as<int64_t>(), stream),
+              "launch cascade candidate selection");
+    check_hip(launch_sort_rows(ws.top_m_ids.as<int64_t>(), batch, m, stream), "launch candidate sort");
+  }
   ws.fine.ensure(sizeof(float) * batch * m, "hipMalloc cascade fine scores");
   fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>());
   check_hip(launch_topk(ws.fine.as<float>(), batch, m, m, k, ws.top_m_ids.as<int64_t>(), d_top_s, d_top_i, stream),
@@ -912,5 +932,30 @@ extern "C" int msim_binary_cascade_topk_async(msim_binary_docs* h, const float* 
     if (batch == 0) return;
     select_device(h->device);
     binres_cascade(h, d_query, batch, query_tokens, k, candidates, d_scores, d_indices, as_stream(stream));
+  });
+}
+
+// ------------------------------------------------- device-resident forms
+
+extern "C" int msim_int4_score_async(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
+                                     const char* reducer, const float* weights, int64_t weights_ndim,
+                                     int64_t weights_dim0, int64_t weights_dim1, double temperature, int residual,
+                                     float* d_out, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    if (h->dim != 128) throw InvalidArgument("device-resident scoring currently requires dim=128");
+    require_shape(batch, query_tokens);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    if (batch == 0 || h->num_docs == 0) return;
+    select_device(h->device);
+    const DocStreams s = int4_streams(h, residual != 0);
+    QueryInput qi;
+    qi.d_query = d_query;
+    qi.limbs = 3;
+    run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, red, (float)temperature, batch, query_tokens,
+                      w.empty() ? nullptr : w.data(), Targets{}, d_out, h->num_docs, nullptr, as_stream(stream));
   });
 }

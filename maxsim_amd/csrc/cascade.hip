@@ -5,6 +5,7 @@
 // rescoring kernel's tile tables are written from them on the device.
 #include "common.hpp"
 #include "internal.hpp"
+#include "topk_block.hpp"
 
 namespace msim {
 
@@ -50,19 +51,16 @@ __global__ __launch_bounds__(256) void candidate_tables_kernel(const int64_t* __
   row[3] = tab0;
 }
 
-// Ascending sort of each row of n <= 4096 int64 values (bitonic, in LDS).
-__global__ __launch_bounds__(1024) void sort_rows_kernel(int64_t* __restrict__ rows, int64_t n, int64_t pow2) {
-  __shared__ int64_t s[kSortMaxRow];
-  int64_t* row = rows + (int64_t)blockIdx.x * n;
-  for (int64_t i = threadIdx.x; i < pow2; i += blockDim.x) s[i] = i < n ? row[i] : INT64_MAX;
-  __syncthreads();
-  for (int64_t size = 2; size <= pow2; size <<= 1) {
-    for (int64_t stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int64_t i = threadIdx.x; i < pow2; i += blockDim.x) {
-        const int64_t j = i ^ stride;
+// Ascending bitonic sort of s[0, pow2) in LDS by the whole block.
+template <typename T>
+__device__ void bitonic_sort(T* s, int pow2) {
+  for (int size = 2; size <= pow2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < pow2; i += blockDim.x) {
+        const int j = i ^ stride;
         if (j > i) {
           const bool up = (i & size) == 0;
-          const int64_t a = s[i], b = s[j];
+          const T a = s[i], b = s[j];
           if ((a > b) == up) {
             s[i] = b;
             s[j] = a;
@@ -72,7 +70,36 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(int64_t* __restrict__ r
       __syncthreads();
     }
   }
+}
+
+// Ascending sort of each row of n <= 4096 int64 values (bitonic, in LDS).
+__global__ __launch_bounds__(1024) void sort_rows_kernel(int64_t* __restrict__ rows, int64_t n, int64_t pow2) {
+  __shared__ int64_t s[kSortMaxRow];
+  int64_t* row = rows + (int64_t)blockIdx.x * n;
+  for (int64_t i = threadIdx.x; i < pow2; i += blockDim.x) s[i] = i < n ? row[i] : INT64_MAX;
+  __syncthreads();
+  bitonic_sort(s, (int)pow2);
   for (int64_t i = threadIdx.x; i < n; i += blockDim.x) row[i] = s[i];
+}
+
+// Per row of n <= 4096 scores: the m best by (score desc, position asc)
+// (the order of _stable_topk, cascade.py:420-453), written as positions in
+// ascending order.  One sort of (descending score key, position) pairs, then
+// one sort of the m selected positions.
+__global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restrict__ scores, int64_t n,
+                                                           int64_t stride, int64_t m, int pow2, int pow2m,
+                                                           int64_t* __restrict__ out) {
+  __shared__ uint64_t keys[kSortMaxRow];
+  __shared__ uint32_t ids[kSortMaxRow];
+  const float* row = scores + (int64_t)blockIdx.x * stride;
+  for (int i = threadIdx.x; i < pow2; i += blockDim.x)
+    keys[i] = i < n ? ((uint64_t)(~score_key(row[i])) << 32) | (uint32_t)i : ~0ull;
+  __syncthreads();
+  bitonic_sort(keys, pow2);
+  for (int i = threadIdx.x; i < pow2m; i += blockDim.x) ids[i] = i < m ? (uint32_t)keys[i] : 0xFFFFFFFFu;
+  __syncthreads();
+  bitonic_sort(ids, pow2m);
+  for (int i = threadIdx.x; i < m; i += blockDim.x) out[(int64_t)blockIdx.x * m + i] = ids[i];
 }
 
 }  // namespace
@@ -84,6 +111,17 @@ hipError_t launch_candidate_tables(const int64_t* d_cands, int64_t m, int64_t gr
   if (n <= 0) return hipSuccess;
   candidate_tables_kernel<<<dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream>>>(
       d_cands, m, groups, d_offsets, waves, per_wave, cap, d_info, d_tiles);
+  return hipGetLastError();
+}
+
+hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, int64_t stride, int64_t m,
+                              int64_t* d_out, hipStream_t stream) {
+  if (batch <= 0 || m <= 0) return hipSuccess;
+  if (n > kSortMaxRow || m > n) return hipErrorInvalidValue;
+  int pow2 = 1, pow2m = 1;
+  while (pow2 < n) pow2 <<= 1;
+  while (pow2m < m) pow2m <<= 1;
+  select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, pow2, pow2m, d_out);
   return hipGetLastError();
 }
 

@@ -119,6 +119,16 @@ struct ScoreArgs {
   float temperature;
   float* pooled;               // pooled[g * pooled_grp_stride + target * grp_rows + row]
   int64_t pooled_grp_stride;
+  // When every pass holds whole batch rows (rows per pass a multiple of
+  // query_tokens, or one batch row per group), the kernel sums each batch
+  // row itself: out[b * out_stride + target] (and iout as int32) instead of
+  // `pooled`.
+  float* out;
+  int64_t out_stride;
+  int32_t* iout;
+  int64_t iout_stride;
+  int32_t query_tokens;
+  bool unit_tscale;            // tscale is all ones (sign documents): integer maximum
 };
 int score_rows_per_pass(int limbs, int64_t rows);
 hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
@@ -143,6 +153,10 @@ hipError_t launch_candidate_tables(const int64_t* d_cands, int64_t m, int64_t gr
                                    int64_t waves, int64_t per_wave, int64_t cap, int64_t* d_info,
                                    uint64_t* d_tiles, hipStream_t stream);
 hipError_t launch_sort_rows(int64_t* d_rows, int64_t batch, int64_t n, hipStream_t stream);
+// The m best of each row of n <= kSortMaxRow scores by (score desc,
+// position asc), output as positions in ascending order [batch, m].
+hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, int64_t stride, int64_t m,
+                              int64_t* d_out, hipStream_t stream);
 
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a

@@ -175,8 +175,14 @@ __device__ __forceinline__ void unpack_a_int4_order(const TileCodes<kDocSign>& t
   }
 }
 
-template <int DOC, bool RES, int L, int NT, int RED>
+// INTMAX (sign documents, one int8 limb, no token scale, MaxSim): the
+// +-1 dot 2 (q8 . bits) - sum(q8) is increasing in the MFMA result, so the
+// running maximum is kept on the int32 accumulators and converted once per
+// document.
+template <int DOC, bool RES, int L, int NT, int RED, bool INTMAX>
 __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
+  static_assert(!INTMAX || (DOC == kDocSign && !RES && L == 1 && RED == kRedMax), "integer maximum form");
+  __shared__ float s_pool[kWavesPerGroup][16 * NT];
   const int lane = lane_id();
   const int wave = wave_uniform(threadIdx.x / kWave);
   const int g = lane >> 4, c = lane & 15;
@@ -212,8 +218,12 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
   const float k2 = kLog2e / p.temperature;
 
   ReducerState<RED> st[NT];
+  int imax[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) st[j].init();
+  for (int j = 0; j < NT; ++j) {
+    st[j].init();
+    imax[j] = INT32_MIN;
+  }
 
   struct Tile {
     TileCodes<DOC> a;
@@ -231,11 +241,13 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
     else
       t.a.w = *reinterpret_cast<const unsigned*>(p.codes + tok * 16 + 4 * g);
     if constexpr (RES) t.r.w = *reinterpret_cast<const v4u*>(p.rcodes + tok * 64 + 16 * g);
+    if constexpr (!INTMAX) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int64_t tr = start + min(4 * g + rr, rows1);
-      t.s[rr] = p.tscale[tr];
-      if constexpr (RES) t.sr[rr] = p.rtscale[tr];
+      for (int rr = 0; rr < 4; ++rr) {
+        const int64_t tr = start + min(4 * g + rr, rows1);
+        t.s[rr] = p.tscale[tr];
+        if constexpr (RES) t.sr[rr] = p.rtscale[tr];
+      }
     }
   };
 
@@ -287,6 +299,18 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
         }
     }
 
+    if constexpr (INTMAX) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        v4i a = acc[0][j];
+        if (rows < 16) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (4 * g + rr >= rows) a[rr] = INT32_MIN;
+        }
+        imax[j] = max(max(imax[j], max(a[0], a[1])), max(a[2], a[3]));
+      }
+    } else {
     float srow[4], srrow[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -323,19 +347,50 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
       }
       st[j].add4(z, k2);
     }
+    }
     len += rows;
 
     if (last) {
       const int64_t tg = t0 + local;
-      float* out = p.pooled + grp * p.pooled_grp_stride + tg * p.grp_rows;
+      float v[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        st[j].merge_xor(16, k2);
-        st[j].merge_xor(32, k2);
-        const float v = st[j].finish(len, colmul[j], p.temperature, weight[j], dscale);
-        const int lr = lr0 + 16 * j + c;
-        if (g == 0 && lr < p.grp_rows) out[lr] = v;
-        st[j].init();
+        if constexpr (INTMAX) {
+          int m = max(imax[j], __shfl_xor(imax[j], 16));
+          m = max(m, __shfl_xor(m, 32));
+          v[j] = len == 0 ? 0.0f : (float)(2 * m - qsum[0][j]) * colmul[j] * weight[j] * dscale;
+          imax[j] = INT32_MIN;
+        } else {
+          st[j].merge_xor(16, k2);
+          st[j].merge_xor(32, k2);
+          v[j] = st[j].finish(len, colmul[j], p.temperature, weight[j], dscale);
+          st[j].init();
+        }
+      }
+      if (p.out || p.iout) {
+        // Whole batch rows in this pass: sum each row's query tokens here
+        // (sequentially from its first token) and write the score.
+        if (g == 0) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) s_pool[wave][16 * j + c] = v[j];
+        }
+        wave_sync_lds();
+        const int nb = min(16 * NT, p.grp_rows - lr0) / p.query_tokens;
+        if (lane < nb) {
+          float sum = 0.0f;
+          for (int q = 0; q < p.query_tokens; ++q) sum += s_pool[wave][lane * p.query_tokens + q];
+          const int64_t b = (grow0 / p.query_tokens) + lane;
+          if (p.out) p.out[b * p.out_stride + tg] = sum;
+          if (p.iout) p.iout[b * p.iout_stride + tg] = (int32_t)sum;
+        }
+        wave_sync_lds();
+      } else {
+        float* out = p.pooled + grp * p.pooled_grp_stride + tg * p.grp_rows;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int lr = lr0 + 16 * j + c;
+          if (g == 0 && lr < p.grp_rows) out[lr] = v[j];
+        }
       }
       len = 0;
     }
@@ -455,11 +510,17 @@ __global__ __launch_bounds__(256) void pool_sum_kernel(const float* __restrict__
 
 template <int DOC, bool RES, int L, int NT>
 hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s) {
+  if constexpr (DOC == kDocSign && !RES && L == 1) {
+    if (reducer == kRedMax && a.unit_tscale) {
+      score_kernel<DOC, RES, L, NT, kRedMax, true><<<grid, kThreads, 0, s>>>(a);
+      return hipGetLastError();
+    }
+  }
   switch (reducer) {
-    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax, false><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2, false><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4, false><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse, false><<<grid, kThreads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -179,3 +179,20 @@ def test_public_binary_routes(gpu, oracle):
     for b in range(2):
         np.testing.assert_array_equal(i[b], _stable(full[b], 8))
         _close(s[b], full[b][i[b]], 1e-6)
+
+
+def test_cascade_over_4096_docs_uses_general_selector(gpu):
+    """More documents than the in-LDS selector holds: radix top-M + row sort."""
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4, prefix_score, residual_int4_to_device, residual_score
+
+    docs, offsets = ragged_fixture(5000, 52, lo=1, hi=6)
+    query = np.random.default_rng(53).standard_normal((2, 4, 128)).astype(np.float32)
+    packed = residual_int4_to_device(pack_residual_int4(docs, offsets))
+    top_s, top_i = cascade_topk(query, packed, 5, candidates=300)
+    coarse = prefix_score(query, packed)
+    for b in range(2):
+        cands = _stable(coarse[b], 300)
+        fine = residual_score(query[b], packed, candidate_indices=cands)
+        order = _stable(fine, 5, tie_ids=cands)
+        np.testing.assert_array_equal(top_i[b], cands[order])
+        np.testing.assert_array_equal(top_s[b], fine[order])
