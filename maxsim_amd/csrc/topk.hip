@@ -176,13 +176,91 @@ __global__ __launch_bounds__(THREADS) void topk_small_kernel(const float* __rest
   }
 }
 
+// ------------------------------------------------------ threshold filter
+// k <= kSmallTopkMaxK and n <= kFilterThreads * kFilterEPT.  Element i of the
+// row goes to thread i % 1024 (coalesced loads).  In each wave, T_w = the
+// k-th largest of the 64 lanes' maximum keys: the wave holds at least k keys
+// >= T_w, so every key of the row's top k is >= T = max_w T_w.  At most k
+// lanes per wave have a maximum >= T (keys are unique), so at most
+// kFilterEPT * k keys per wave pass the filter; wave 0 selects the k best of
+// them in k rounds of a wave maximum.
+constexpr int kFilterThreads = 1024;
+constexpr int kFilterEPT = 4;
+constexpr int kFilterWaves = kFilterThreads / kWave;
+constexpr int kFilterCap = kFilterWaves * kFilterEPT * kSmallTopkMaxK;
+
+__global__ __launch_bounds__(kFilterThreads) void topk_filter_kernel(const float* __restrict__ scores, int64_t n,
+                                                                     int64_t row_stride, int32_t k,
+                                                                     const int64_t* __restrict__ id_map,
+                                                                     float* __restrict__ out_scores,
+                                                                     int64_t* __restrict__ out_ids) {
+  __shared__ uint64_t s_cand[kFilterCap];
+  __shared__ uint64_t s_thr[kFilterWaves];
+  __shared__ uint64_t s_best[kSmallTopkMaxK];
+  __shared__ uint32_t s_count;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int64_t b = blockIdx.x;
+  const float* row = scores + b * row_stride;
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
+  float v[kFilterEPT];
+#pragma unroll
+  for (int e = 0; e < kFilterEPT; ++e) v[e] = __uint_as_float(load_b32(rsrc, (e * kFilterThreads + tid) * 4));
+  if (tid == 0) s_count = 0;
+  uint64_t key[kFilterEPT], lmax = 0;
+#pragma unroll
+  for (int e = 0; e < kFilterEPT; ++e) {
+    const int i = e * kFilterThreads + tid;
+    key[e] = i < n ? ((uint64_t)score_key(v[e]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0u;
+    lmax = key[e] > lmax ? key[e] : lmax;
+  }
+  // T_w: k rounds of the wave maximum over the lanes' maxima.
+  uint64_t m = lmax, kth = 0;
+  for (int r = 0; r < k; ++r) {
+    kth = wave_max_u64(m);
+    if (m == kth) m = 0;
+  }
+  if (lane == 0) s_thr[wave] = kth;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kFilterWaves; ++w) t = s_thr[w] > t ? s_thr[w] : t;
+#pragma unroll
+  for (int e = 0; e < kFilterEPT; ++e) {
+    if (key[e] != 0 && key[e] >= t) s_cand[atomicAdd(&s_count, 1u)] = key[e];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int c = (int)s_count;
+    for (int r = 0; r < k; ++r) {
+      uint64_t best = 0;
+      int slot = -1;
+      for (int j = lane; j < c; j += kWave) {
+        const uint64_t x = s_cand[j];
+        if (x > best) {
+          best = x;
+          slot = j;
+        }
+      }
+      const uint64_t top = wave_max_u64(best);
+      if (slot >= 0 && best == top) s_cand[slot] = 0;  // the one lane holding it drops it
+      if (lane == 0) s_best[r] = top;
+    }
+  }
+  __syncthreads();
+  if (tid < k) {
+    const int64_t pos = (int64_t)(0xFFFFFFFFu - (uint32_t)s_best[tid]);
+    out_scores[b * k + tid] = row[pos];
+    out_ids[b * k + tid] = id_map ? id_map[b * n + pos] : pos;
+  }
+}
+
 hipError_t launch_topk(const float* d_scores, int64_t batch, int64_t n, int64_t row_stride,
                        int64_t k, const int64_t* d_id_map, float* d_out_scores,
                        int64_t* d_out_ids, hipStream_t stream) {
   if (batch == 0 || k == 0) return hipSuccess;
   if (k > kTopkMaxK || k > n) return hipErrorInvalidValue;
-  if (k <= kSmallTopkMaxK && n <= 256 * kSmallEPT) {
-    topk_small_kernel<256><<<dim3((unsigned)batch), dim3(256), 0, stream>>>(
+  if (k <= kSmallTopkMaxK && n <= kFilterThreads * kFilterEPT) {
+    topk_filter_kernel<<<dim3((unsigned)batch), dim3(kFilterThreads), 0, stream>>>(
         d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
   } else if (k <= kSmallTopkMaxK && n <= 1024 * kSmallEPT) {
     topk_small_kernel<1024><<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(
