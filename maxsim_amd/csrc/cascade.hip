@@ -82,24 +82,110 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(int64_t* __restrict__ r
   for (int64_t i = threadIdx.x; i < n; i += blockDim.x) row[i] = s[i];
 }
 
+// Block-wide exclusive prefix sum of one value per thread (1024 threads):
+// wave scans by shuffles, then the wave totals.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == kWave - 1) s_wave[wave] = x;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+    const uint32_t t = s_wave[w];
+    before += w < wave ? t : 0u;
+    all += t;
+  }
+  __syncthreads();
+  total = all;
+  return before + x - v;
+}
+
 // Per row of n <= 4096 scores: the m best by (score desc, position asc)
 // (the order of _stable_topk, cascade.py:420-453), written as positions in
-// ascending order.  One sort of (descending score key, position) pairs, then
-// one sort of the m selected positions.
+// ascending order.  Radix selection of the m-th largest order-preserving
+// score key, 8 bits per round, then a stable compaction: keys above it, and
+// the first `need` keys equal to it in position order.
 __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restrict__ scores, int64_t n,
-                                                           int64_t stride, int64_t m, int pow2, int pow2m,
-                                                           int64_t* __restrict__ out) {
-  __shared__ uint64_t keys[kSortMaxRow];
-  __shared__ uint32_t ids[kSortMaxRow];
+                                                           int64_t stride, int64_t m, int64_t* __restrict__ out) {
+  constexpr int E = kSortMaxRow / 1024;  // positions 4 t .. 4 t + 3 of thread t
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_digit, s_above;
+  const int tid = threadIdx.x, lane = tid % kWave;
   const float* row = scores + (int64_t)blockIdx.x * stride;
-  for (int i = threadIdx.x; i < pow2; i += blockDim.x)
-    keys[i] = i < n ? ((uint64_t)(~score_key(row[i])) << 32) | (uint32_t)i : ~0ull;
-  __syncthreads();
-  bitonic_sort(keys, pow2);
-  for (int i = threadIdx.x; i < pow2m; i += blockDim.x) ids[i] = i < m ? (uint32_t)keys[i] : 0xFFFFFFFFu;
-  __syncthreads();
-  bitonic_sort(ids, pow2m);
-  for (int i = threadIdx.x; i < m; i += blockDim.x) out[(int64_t)blockIdx.x * m + i] = ids[i];
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
+  uint32_t key[E];
+  bool valid[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = E * tid + e;
+    valid[e] = i < n;
+    key[e] = score_key(__uint_as_float(load_b32(rsrc, i * 4)));
+  }
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)m;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += blockDim.x) s_hist[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&s_hist[(key[e] >> shift) & 255u], 1u);
+    __syncthreads();
+    if (tid < kWave) {
+      // Lane l holds digits 4l .. 4l + 3; suffix sums over the lanes from
+      // the top digit down find the digit where the count reaches `need`.
+      uint32_t c[4], local = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = s_hist[4 * lane + j];
+        local += c[j];
+      }
+      uint32_t suffix = local;  // inclusive: lanes >= this one
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t y = __shfl_down(suffix, d);
+        if (lane + d < kWave) suffix += y;
+      }
+      uint32_t above = suffix - local;  // digits of higher lanes
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        if (above < need && above + c[j] >= need) {
+          s_digit = (uint32_t)(4 * lane + j);
+          s_above = above;
+        }
+        above += c[j];
+      }
+    }
+    __syncthreads();
+    prefix |= s_digit << shift;
+    mask |= 0xFFu << shift;
+    need -= s_above;
+    __syncthreads();
+  }
+  // Stable compaction in position order.
+  uint32_t eq = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) eq += (valid[e] && key[e] == prefix) ? 1u : 0u;
+  uint32_t total;
+  uint32_t tie_rank = block_exclusive_scan(eq, s_wave, total);
+  uint32_t sel = 0;
+  bool take[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const bool tie = valid[e] && key[e] == prefix;
+    take[e] = valid[e] && (key[e] > prefix || (tie && tie_rank < need));
+    tie_rank += tie ? 1u : 0u;
+    sel += take[e] ? 1u : 0u;
+  }
+  uint32_t rank = block_exclusive_scan(sel, s_wave, total);
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (take[e]) out[(int64_t)blockIdx.x * m + rank++] = E * tid + e;
+  (void)lane;
 }
 
 }  // namespace
@@ -118,10 +204,7 @@ hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, i
                               int64_t* d_out, hipStream_t stream) {
   if (batch <= 0 || m <= 0) return hipSuccess;
   if (n > kSortMaxRow || m > n) return hipErrorInvalidValue;
-  int pow2 = 1, pow2m = 1;
-  while (pow2 < n) pow2 <<= 1;
-  while (pow2m < m) pow2m <<= 1;
-  select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, pow2, pow2m, d_out);
+  select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, d_out);
   return hipGetLastError();
 }
 
