@@ -141,6 +141,14 @@ int msim_int4_score(msim_int4_docs* h, const float* query, int64_t batch, int64_
                     int64_t weights_dim0, int64_t weights_dim1, double temperature,
                     const int64_t* candidates, int64_t num_candidates, int residual, float* out);
 
+/* Top-k of msim_int4_score over every document, selected on the device
+ * (the reference selects non-MaxSim reducers on the host,
+ * experimental.py:523-535). */
+int msim_int4_topk_score(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                         int64_t dim, int64_t k, const char* reducer, const float* weights,
+                         int64_t weights_ndim, int64_t weights_dim0, int64_t weights_dim1,
+                         double temperature, int residual, float* out_scores, int64_t* out_indices);
+
 /* Device-resident form of msim_int4_score over every document (dim 128):
  * d_query f32 [B, Q, 128] and d_out f32 [B, N] on the device; weights as
  * msim_int4_score (host memory, read during the call); enqueued on
@@ -224,6 +232,15 @@ int msim_binary_score(msim_binary_docs* h, const float* query, int64_t batch,
                       int use_scale_vector, int use_token_scale,
                       const float* scale_vector_override, const int64_t* candidates,
                       int64_t num_candidates, float* out);
+/* Top-k of msim_binary_score over every document, selected on the device
+ * (the reference selects non-MaxSim reducers on the host, _api.py:481-497). */
+int msim_binary_topk_score(msim_binary_docs* h, const float* query, int64_t batch,
+                           int64_t query_tokens, int64_t dim, int64_t k, const char* reducer,
+                           const float* weights, int64_t weights_ndim, int64_t weights_dim0,
+                           int64_t weights_dim1, double temperature, double scale,
+                           int use_scale_vector, int use_token_scale,
+                           const float* scale_vector_override, float* out_scores,
+                           int64_t* out_indices);
 /* Sign-binarised queries (XOR / popcount): qbits u8[B, Q, dim/8] in the
  * pack_signs bit order.  Scores are sum_q max_t (dim - 2 popcount(q ^ d)),
  * exactly what maxsim_batch returns for the +/-1 query (no reference kernel;

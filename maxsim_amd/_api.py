@@ -403,12 +403,18 @@ def topk_maxsim(query_tokens, packed: PackedDocs, k: int, *, scale=None, device=
             scores, indices = resident.data.topk_batch(np.ascontiguousarray(batches, dtype=np.float32), int(k),
                                                        float(resolved_scale), False, use_token_scale)
         return (scores[0], indices[0]) if squeeze else (scores, indices)
-    full = score(query, packed if packed.device == "cpu" else resident, scale=scale, device=device,
-                 reducer=reducer_value, query_weights=weights, temperature=temperature_value)
-    full2 = full[None, :] if full.ndim == 1 else full
-    order = np.stack([_topk_indices_1d(row, k) for row in full2])
-    scores = np.take_along_axis(full2, order, axis=1)
-    return (scores[0], order[0]) if full.ndim == 1 else (scores, order)
+    if batches.shape[1] == 0:
+        zeros = np.zeros((batches.shape[0], packed.num_docs), np.float32)
+        order = np.stack([_topk_indices_1d(row, k) for row in zeros])
+        scores = np.take_along_axis(zeros, order, axis=1)
+        return (scores[0], order[0]) if squeeze else (scores, order)
+    # Any reducer: scores and the selection stay on the device.
+    vector = resolved_scale if _scale_is_vector(resolved_scale) else None
+    kernel_scale = 1.0 if vector is not None else float(resolved_scale)
+    scores, indices = resident.data.topk_score_batch(np.ascontiguousarray(batches, dtype=np.float32), int(k),
+                                                     reducer_value, weights, float(temperature_value), kernel_scale,
+                                                     False, use_token_scale, vector)
+    return (scores[0], indices[0]) if squeeze else (scores, indices)
 
 
 def pack_query_signs(query) -> np.ndarray:

@@ -178,6 +178,21 @@ class CudaInt4PackedDocs:
                                         query_weights=None, temperature=1.0):
         return self._score(query, candidate_indices, reducer, query_weights, temperature, True)
 
+    def topk_score_batch(self, query, k, reducer="maxsim", query_weights=None, temperature=1.0, residual=False):
+        """Top-k under any reducer, selected on the device."""
+        q = _query3(query)
+        w, wnd, w0, w1 = _weights(query_weights)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        if not isinstance(reducer, str):
+            raise ValueError("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(self._lib.msim_int4_topk_score(self._h, ptr(q), *q.shape, k, reducer.encode(), ptr(w), wnd, w0, w1,
+                                             float(temperature), 1 if residual else 0, ptr(scores), ptr(indices)))
+        return scores, indices
+
     def cascade_topk(self, query, k, candidates, reducer="maxsim", query_weights=None, temperature=1.0):
         """Prefix top-M -> fused residual rescoring -> top-k, all on the device
         (the pipeline of cascade_topk, cascade.py:294-393)."""
@@ -384,6 +399,28 @@ class CudaPackedDocs:
                                scale_vector_override=None):
         return self._score(query, candidate_indices, reducer, query_weights, temperature, scale,
                            use_scale_vector, use_token_scale, scale_vector_override)
+
+    def topk_score_batch(self, query, k, reducer="maxsim", query_weights=None, temperature=1.0, scale=1.0,
+                         use_scale_vector=False, use_token_scale=False, scale_vector_override=None):
+        """Top-k under any reducer, selected on the device."""
+        q = _query3(query)
+        w, wnd, w0, w1 = _weights(query_weights)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        override = None
+        if scale_vector_override is not None:
+            override = _f32(scale_vector_override)
+            if override.ndim != 1 or override.shape[0] != self.num_docs:
+                raise ValueError("scale vector must have shape [num_docs]")
+        if not isinstance(reducer, str):
+            raise ValueError("reducer must be one of 'maxsim', 'weighted_maxsim', 'topk2', 'topk4', or 'smoothsim'")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(self._lib.msim_binary_topk_score(self._h, ptr(q), *q.shape, k, reducer.encode(), ptr(w), wnd, w0, w1,
+                                               float(temperature), float(scale), int(bool(use_scale_vector)),
+                                               int(bool(use_token_scale)), ptr(override), ptr(scores), ptr(indices)))
+        return scores, indices
 
     # ------------------------------------------------- sign-bit queries
     def hamming_batch(self, qbits):

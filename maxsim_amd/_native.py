@@ -45,6 +45,10 @@ SIGNATURES: dict[str, list] = {
     "msim_int4_topk_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_int4_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl,
                         c_vp, c_i64, c_int, c_vp],
+    "msim_int4_topk_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl, c_int,
+                             c_vp, c_vp],
+    "msim_binary_topk_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl, c_dbl,
+                               c_int, c_int, c_vp, c_vp, c_vp],
     "msim_int4_score_async": [c_vp, c_vp, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64, c_dbl, c_int, c_vp,
                               c_vp],
     "msim_int4_cascade_topk": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_str, c_vp, c_i64, c_i64, c_i64,

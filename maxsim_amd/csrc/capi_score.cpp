@@ -959,3 +959,60 @@ extern "C" int msim_int4_score_async(msim_int4_docs* h, const float* d_query, in
                       w.empty() ? nullptr : w.data(), Targets{}, d_out, h->num_docs, nullptr, as_stream(stream));
   });
 }
+
+// ------------------------------------------- top-k under any reducer
+
+extern "C" int msim_int4_topk_score(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                    int64_t dim, int64_t k, const char* reducer, const float* weights,
+                                    int64_t weights_ndim, int64_t weights_dim0, int64_t weights_dim1,
+                                    double temperature, int residual, float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_dim(dim, h->dim);
+    require_shape(batch, query_tokens);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    if (residual && !h->has_residual)
+      throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
+    if (batch == 0) return;
+    select_device(h->device);
+    float* d = int4_score_device(h, query, batch, query_tokens, dim, red, w, (float)temperature, nullptr, 0,
+                                 residual != 0, nullptr);
+    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
+    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
+                          h->top_indices.as<int64_t>(), nullptr),
+              "launch topk selection kernel");
+    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+  });
+}
+
+extern "C" int msim_binary_topk_score(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                      int64_t dim, int64_t k, const char* reducer, const float* weights,
+                                      int64_t weights_ndim, int64_t weights_dim0, int64_t weights_dim1,
+                                      double temperature, double scale, int use_scale_vector, int use_token_scale,
+                                      const float* scale_vector_override, float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_binary_query(h, batch, query_tokens, dim);
+    const int red = parse_reducer(reducer);
+    check_temperature(temperature);
+    const std::vector<float> w =
+        row_weights(reducer, weights, weights_ndim, weights_dim0, weights_dim1, batch, query_tokens);
+    if (batch == 0) return;
+    select_device(h->device);
+    const float* d_override = nullptr;
+    if (scale_vector_override) {
+      std::vector<float> v(scale_vector_override, scale_vector_override + h->num_docs);
+      d_override = upload_vec(h->scale_override, v, "copy scale vector override to device");
+    }
+    const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, d_override);
+    float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, red, w, (float)temperature,
+                                   nullptr, 0);
+    copy_topk_out(h, d, batch, k, out_scores, out_indices, nullptr);
+  });
+}

@@ -223,11 +223,11 @@ def topk_int4_maxsim(query_tokens, packed: Int4PackedDocs, k: int, *, device="au
         scores, indices = resident.data.topk_batch_int8q(query, int(k))
     elif reducer_value == "maxsim":
         scores, indices = resident.data.topk_batch(query, int(k))
+    elif batches.shape[1] == 0:
+        scores, indices = _topk_rows(np.zeros((batches.shape[0], packed.num_docs), np.float32), k)
     else:
-        scores, indices = _topk_rows(
-            _int4_score(query, resident, device="cuda", reducer=reducer_value,
-                        query_weights=weights, temperature=temperature_value,
-                        candidate_indices=None, force_generalized=False), k)
+        scores, indices = resident.data.topk_score_batch(query, int(k), reducer_value, weights,
+                                                         float(temperature_value))
     return (scores[0], indices[0]) if squeeze else (scores, indices)
 
 

@@ -196,3 +196,27 @@ def test_cascade_over_4096_docs_uses_general_selector(gpu):
         order = _stable(fine, 5, tie_ids=cands)
         np.testing.assert_array_equal(top_i[b], cands[order])
         np.testing.assert_array_equal(top_s[b], fine[order])
+
+
+@pytest.mark.parametrize("reducer", ["weighted_maxsim", "topk2", "smoothsim"])
+def test_public_topk_under_reducers_selects_on_device(gpu, reducer):
+    """topk_maxsim / topk_int4_maxsim with a non-MaxSim reducer: the device
+    selection equals the stable order of the full scores (_api.py:481-497,
+    experimental.py:523-535)."""
+    import maxsim_amd as ms
+
+    docs, offsets = ragged_fixture(90, 54, lo=1, hi=25)
+    rng = np.random.default_rng(55)
+    query = rng.standard_normal((3, 5, 128)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, size=(3, 5)).astype(np.float32) if reducer == "weighted_maxsim" else None
+    kw = dict(reducer=reducer, query_weights=w, temperature=0.6)
+    for packed, top, full in (
+        (ms.pack_signs(docs, offsets, scale="doc", token_scale="mean_abs"), ms.topk_maxsim, ms.maxsim),
+        (ms.pack_int4_symmetric(docs, offsets, scale_granularity="token"), ms.topk_int4_maxsim, ms.int4_maxsim),
+    ):
+        s, i = top(query, packed, 7, **kw)
+        f = full(query, packed, **kw)
+        for b in range(3):
+            order = _stable(f[b], 7)
+            np.testing.assert_array_equal(i[b], order)
+            np.testing.assert_array_equal(s[b], f[b][order])
