@@ -9,8 +9,8 @@ it resident on the GPU once and ``search`` / ``rerank`` return
 Modes: the reference's binary, binary_token_scale(_u8, _u4), pooled_binary,
 int4, int4_per_token and int4_residual, plus ``binary_residual`` (sign-bit
 prefix with a per-token scale + per-token int4 residual; see
-``maxsim_amd.binres``).  ``binary_q40`` and index files (``save`` / ``load``)
-are not provided.
+``maxsim_amd.binres``).  Index files use the reference's .npz format
+(``maxsim_amd.index_io``).  ``binary_q40`` is not provided.
 """
 from __future__ import annotations
 
@@ -153,11 +153,17 @@ class Corpus:
         return self.encoded_bytes
 
     def save(self, path) -> None:
-        raise NotImplementedError("index files are not supported by maxsim_amd")
+        """Write the reference's .npz index format (sdk.py:203-288)."""
+        from maxsim_amd.index_io import save_corpus
+
+        save_corpus(self, path)
 
     @classmethod
     def load(cls, path) -> "Corpus":
-        raise NotImplementedError("index files are not supported by maxsim_amd")
+        """Read a .npz index of schema version 1 or 2 (sdk.py:290-410)."""
+        from maxsim_amd.index_io import load_corpus
+
+        return load_corpus(path)
 
 
 Index = Corpus
@@ -186,6 +192,11 @@ class Reranker:
     def from_corpus(cls, corpus: Corpus, *, device: Literal["cpu", "cuda"] = "cuda",
                     int4_query: Literal["fp32", "int8"] = "fp32") -> "Reranker":
         return cls(corpus, device=device, int4_query=int4_query)
+
+    @classmethod
+    def load(cls, path, *, device: Literal["cpu", "cuda"] = "cuda",
+             int4_query: Literal["fp32", "int8"] = "fp32") -> "Reranker":
+        return cls.from_corpus(Corpus.load(path), device=device, int4_query=int4_query)
 
     def search(self, query_embeddings, *, k: int = 10, rescore_candidates: int | None = None,
                reducer: str = "maxsim", query_weights=None, temperature: float = 1.0):

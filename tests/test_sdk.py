@@ -90,3 +90,94 @@ def test_reranker_cpu_device_is_rejected():
         maxsim.Reranker(c, device="cpu")
     with pytest.raises(ValueError, match="int4_query"):
         maxsim.Reranker(c, int4_query="fp16")
+
+
+@pytest.mark.parametrize("mode", ["binary", "binary_token_scale", "binary_token_scale_u8", "binary_token_scale_u4",
+                                  "pooled_binary", "int4", "int4_per_token", "int4_residual", "binary_residual"])
+def test_save_load_roundtrip(tmp_path, mode):
+    rng = np.random.default_rng(11)
+    docs = rng.standard_normal((30, 16)).astype(np.float32)
+    offsets = np.array([0, 5, 5, 12, 30], dtype=np.int64)
+    ids = ["a", "b", "c", "d"]
+    c = maxsim.Corpus.from_embeddings(ids, docs, offsets, mode=mode, metadata={"k": 1})
+    path = tmp_path / f"{mode}.maxsim.npz"
+    c.save(path)
+    back = maxsim.Corpus.load(path)
+    assert back.mode == mode and back.doc_ids == tuple(ids) and back.metadata == c.metadata
+    assert back.encoded_bytes == c.encoded_bytes
+    a, b = (c.packed, back.packed) if c.packed is not None else (c.int4_packed, back.int4_packed)
+    for name in ("data", "sign_data", "prefix_data", "residual_data", "values", "residual_values", "prefix_values",
+                 "doc_offsets", "token_scale", "prefix_token_scale", "residual_token_scale", "prefix_scale"):
+        x, y = getattr(a, name, None), getattr(b, name, None)
+        if isinstance(x, np.ndarray):
+            tol = 2e-3 if name == "token_scale" and mode != "int4_per_token" else 0
+            np.testing.assert_allclose(y, x, rtol=tol, atol=0)
+
+
+def test_load_accepts_schema_v1(tmp_path):
+    """tests/test_sdk.py:465-486."""
+    docs = np.array([[1] * 8, [-1] * 8, [1, -1] * 4], dtype=np.float32)
+    offsets = np.array([0, 1, 2, 3], dtype=np.int64)
+    packed = maxsim.pack_int4_symmetric(docs, offsets)
+    path = tmp_path / "legacy.npz"
+    np.savez_compressed(path, schema_version=np.array(1, dtype=np.int64), format=np.array("maxsim_corpus"),
+                        mode=np.array("int4"), doc_ids=np.array(["p", "n", "m"]), metadata_json=np.array("{}"),
+                        int4_data=packed.data, doc_offsets=offsets, dim=np.array(8, dtype=np.int64),
+                        int4_scale=np.array(packed.scale, dtype=np.float32))
+    np.testing.assert_array_equal(maxsim.Corpus.load(path).int4_packed.values, packed.values)
+
+
+def _resave(tmp_path, mode, edit):
+    docs = np.array([[1] * 8, [-1] * 8, [1, -1] * 4], dtype=np.float32)
+    path = tmp_path / "valid.npz"
+    maxsim.Corpus.from_embeddings(["a", "b", "c"], docs, np.array([0, 1, 2, 3]), mode=mode).save(path)
+    with np.load(path, allow_pickle=False) as data:
+        payload = {k: np.asarray(data[k]) for k in data.files}
+    edit(payload)
+    bad = tmp_path / "bad.npz"
+    np.savez_compressed(bad, **payload)
+    return bad
+
+
+@pytest.mark.parametrize("offsets,message", [([1, 1, 2, 3], "start at 0"), ([0, 2, 1, 3], "monotonically"),
+                                             ([0, 1, 2, 4], "end at num_doc_tokens")])
+def test_load_rejects_corrupt_offsets(tmp_path, offsets, message):
+    """tests/test_sdk.py:518-540."""
+    bad = _resave(tmp_path, "binary", lambda p: p.__setitem__("doc_offsets", np.array(offsets, dtype=np.int64)))
+    with pytest.raises(ValueError, match=message):
+        maxsim.Corpus.load(bad)
+
+
+def test_load_rejects_bad_dtypes_and_negative_eight(tmp_path):
+    """tests/test_sdk.py:543-593."""
+    bad = _resave(tmp_path, "binary", lambda p: p.__setitem__("packed_data", p["packed_data"].astype(np.float32)))
+    with pytest.raises(ValueError, match="dtype uint8"):
+        maxsim.Corpus.load(bad)
+    bad = _resave(tmp_path, "int4_per_token",
+                  lambda p: p.__setitem__("int4_token_scale", p["int4_token_scale"].astype(np.float64)))
+    with pytest.raises(ValueError, match="dtype float32"):
+        maxsim.Corpus.load(bad)
+
+    def eight(p):
+        p["int4_data"] = p["int4_data"].copy()
+        p["int4_data"][0, 0] = (p["int4_data"][0, 0] & 0xF0) | 0x08
+
+    with pytest.raises(ValueError, match="symmetric int4"):
+        maxsim.Corpus.load(_resave(tmp_path, "int4", eight))
+
+
+def test_save_rejects_invalid_payloads(tmp_path):
+    """tests/test_sdk.py:596-627."""
+    from dataclasses import replace
+
+    docs = np.array([[1] * 8, [-1] * 8, [1, -1] * 4], dtype=np.float32)
+    c = maxsim.Corpus.from_embeddings(["a", "b", "c"], docs, np.array([0, 1, 2, 3]), mode="int4_per_token")
+    data = c.int4_packed.data.copy()
+    data[0, 0] ^= np.uint8(1)
+    with pytest.raises(ValueError, match="does not encode"):
+        replace(c, int4_packed=replace(c.int4_packed, data=data)).save(tmp_path / "x.npz")
+    packed = maxsim.pack_signs(docs)
+    invalid = maxsim.PackedDocs(data=packed.data, doc_offsets=np.array([0, 2, 1, 3], dtype=np.int64),
+                                dim=packed.dim, num_docs=packed.num_docs)
+    with pytest.raises(ValueError, match="monotonically"):
+        maxsim.Corpus(doc_ids=("a", "b", "c"), mode="binary", packed=invalid).save(tmp_path / "y.npz")
