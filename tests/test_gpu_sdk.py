@@ -102,3 +102,24 @@ def test_binary_residual_mode(gpu, oracle):
         got = np.array([x.score for x in full[b]])
         idx = [ids.index(x.doc_id) for x in full[b]]
         np.testing.assert_allclose(got, exp[b][idx], rtol=1e-6, atol=1e-5)
+
+
+@pytest.mark.parametrize("mode", ["binary_token_scale", "int4_per_token", "int4_residual", "binary_residual"])
+def test_saved_index_searches_the_same(gpu, tmp_path, mode):
+    """tests/test_sdk.py:130-306: an index read back from its .npz file gives
+    the same results."""
+    rng = np.random.default_rng(199)
+    docs = rng.normal(size=(40, 128)).astype(np.float32)
+    offsets = np.array([0, 3, 5, 9, 12, 20, 40], dtype=np.int64)
+    ids = list("abcdef")
+    query = rng.normal(size=(2, 4, 128)).astype(np.float32)
+    index = maxsim.Index.from_embeddings(ids, docs, offsets, mode=mode)
+    index.save(tmp_path / "i.npz")
+    loaded = maxsim.Index.load(tmp_path / "i.npz")
+    kw = {"rescore_candidates": 4} if mode in {"int4_residual", "binary_residual"} else {}
+    a = maxsim.Reranker(index, device="cuda").search(query, k=3, **kw)
+    b = maxsim.Reranker.load(tmp_path / "i.npz", device="cuda").search(query, k=3, **kw)
+    assert [[x.doc_id for x in r] for r in a] == [[x.doc_id for x in r] for r in b]
+    np.testing.assert_allclose([[x.score for x in r] for r in a], [[x.score for x in r] for r in b], rtol=0,
+                               atol=1e-5 if mode == "binary_token_scale" else 0)
+    assert loaded.encoded_bytes == index.encoded_bytes
