@@ -214,7 +214,7 @@ void build_wave_info(msim_int4_docs* h, int64_t waves) {
   if (h->partition_waves == waves) return;
   std::vector<int64_t> info;
   std::vector<uint64_t> tiles;
-  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, tiles);
+  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, tiles, h->tile_stride);
   h->num_scan_waves = (int64_t)info.size() / kWaveInfoWords;
   h->wave_info.ensure(sizeof(int64_t) * std::max<size_t>(1, info.size()), "hipMalloc scan wave table");
   if (!info.empty())
@@ -231,7 +231,7 @@ int64_t scan_waves(const msim_int4_docs* h) {
   // Default: eight waves per CU (two per SIMD); a docs-per-wave override sets
   // the count directly.
   int64_t waves = g_docs_per_wave > 0 ? (h->num_docs + g_docs_per_wave - 1) / g_docs_per_wave
-                                      : (int64_t)device_cu_count() * 8;
+                                      : (int64_t)device_cu_count() * kScanWavesPerCu;
   return std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
 }
 
@@ -252,11 +252,15 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
   a.offsets = h->offsets.as<int64_t>();
   a.wave_info = h->wave_info.as<int64_t>();
   a.tile_table = h->tile_table.as<uint64_t>();
+  a.tile_stride = h->tile_stride;
   a.num_waves = h->num_scan_waves;
   a.query_tokens = (int32_t)query_tokens;
   a.scale = h->scale;
   a.score_stride = h->num_docs;
-  const int64_t per_pass = 128 / query_tokens;
+#ifndef MSIM_SCAN_PASS_ROWS
+#define MSIM_SCAN_PASS_ROWS 128
+#endif
+  const int64_t per_pass = std::max<int64_t>(1, MSIM_SCAN_PASS_ROWS / query_tokens);
   for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
     const int64_t nb = std::min(per_pass, batch - b0);
     a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;

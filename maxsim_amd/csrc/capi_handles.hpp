@@ -87,6 +87,7 @@ struct msim_int4_docs {
   std::vector<int64_t> host_offsets;
   int64_t partition_waves = 0;    // wave count the cached scan table was built for
   int64_t num_scan_waves = 0;     // rows of wave_info
+  int64_t tile_stride = 0;        // tile-table entries per wave
   msim::DeviceBuffer wave_info, tile_table;
   msim::DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales16;
   // Generalized path: codes padded to 64 bytes per token when dim < 128,

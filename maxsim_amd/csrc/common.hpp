@@ -145,6 +145,14 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
 }
 
 __device__ __forceinline__ float fmax3(float a, float b, float c) { return fmaxf(a, fmaxf(b, c)); }
+// One v_max3_f32 (the compiler splits fmax chains into two-operand maxima to
+// shorten dependencies; where issue slots are the limit, one instruction per
+// three operands is better).  Operands are never NaN in these kernels.
+__device__ __forceinline__ float max3_op(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // numpy's pairwise float64 reduction order over a[0..n) for 8 < n <= 128 is
 // eight strided accumulators, combined ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),

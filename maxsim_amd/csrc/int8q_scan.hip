@@ -87,8 +87,14 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
   }
 }
 
+#ifdef MSIM_SCAN_WAVES_PER_EU
+#define MSIM_SCAN_OCCUPANCY __attribute__((amdgpu_waves_per_eu(MSIM_SCAN_WAVES_PER_EU, MSIM_SCAN_WAVES_PER_EU)))
+#else
+#define MSIM_SCAN_OCCUPANCY
+#endif
+
 template <int NT, bool kTS>
-__global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
+__global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_kernel(
     ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale16,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
     const uint64_t* __restrict__ tile_table, const int8_t* __restrict__ qpack,
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
   const int ndocs = (int)info[1];
   const int64_t T0 = info[2], T1 = info[3];
   const int ntiles = (int)info[4];
-  const auto tt = as_constant(tile_table) + info[5];
+  const auto tt = as_constant(tile_table) + gw * p.tile_stride;  // no wait on `info`
   const bool has_empty = info[6] != 0;
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
       const float x1 = (float)acc[par][j][1] * sc[par][1];
       const float x2 = (float)acc[par][j][2] * sc[par][2];
       const float x3 = (float)acc[par][j][3] * sc[par][3];
-      m[j] = fmaxf(fmaxf(fmaxf(m[j], x0), x1), fmaxf(x2, x3));
+      m[j] = max3_op(max3_op(m[j], x0, x1), x2, x3);
     }
   };
   // Document end: per-row maxima over the four lane groups, then the score of
@@ -269,11 +275,13 @@ __global__ __launch_bounds__(kScanThreads) void int8q_scan_kernel(
     vm_wait_lds<kRingWait>();
     w = s_codes[wave][slot][lane];
     if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
+    // All first halves, then all second halves: consecutive MFMAs are
+    // independent, so the matrix pipe never waits on its own result.
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+    for (int j = 0; j < NT; ++j) acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
       acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc[par][j], 0, 0, 0);
-    }
     if (has_prev) {
       epilogue_max(par ^ 1);
       // One MFMA, then five VALU instructions of the previous tile's epilogue.

@@ -59,13 +59,18 @@ constexpr int kScanWavesPerGroup = 4;
 #define MSIM_SCAN_PREFETCH 8
 #endif
 constexpr int kScanPrefetch = MSIM_SCAN_PREFETCH;  // ring depth: tiles in flight per wave
+#ifndef MSIM_SCAN_WAVES_PER_CU
+#define MSIM_SCAN_WAVES_PER_CU 8
+#endif
+constexpr int kScanWavesPerCu = MSIM_SCAN_WAVES_PER_CU;  // scan waves launched per CU
 constexpr uint32_t kScanPastEnd = 0x3FFFFF0u;      // (kScanPastEnd + 15) * 64 + 48 < 2^32
 struct ScanArgs {
   const uint8_t* codes;         // [num_tokens, 64] int4 nibbles
   const float* token_scale16;   // [num_tokens] token scales / 16, or nullptr (tensor scale)
   const int64_t* offsets;       // [num_docs + 1]
   const int64_t* wave_info;     // [num_waves, kWaveInfoWords]
-  const uint64_t* tile_table;   // per-wave tile entries
+  const uint64_t* tile_table;   // per-wave tile entries, wave w's at w * tile_stride
+  int64_t tile_stride;
   int64_t num_waves;            // a multiple of kScanWavesPerGroup
   const int8_t* qpack;          // >= rows + 128 rows of MFMA B-order int8 codes (zero past rows)
   const float* qscale;          // per-row query scale, same row count
@@ -78,9 +83,10 @@ struct ScanArgs {
 hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream);
 // Builds the wave table and tile table for `waves` requested waves (the
 // result may hold more rows: ranges are split at kScanMaxDocsPerWave
-// documents and 2^25 tokens, and padded to whole workgroups).
+// documents and 2^25 tokens, and padded to whole workgroups).  Each wave's
+// tile entries start at wave * tile_stride.
 void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves,
-                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table);
+                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table, int64_t& tile_stride);
 
 // Generalized scoring (score.hip): int4 or sign-bit documents, optional int4
 // residual stream, 1 (int8) or 3 (fp32 split into int8 limbs) query limbs,

@@ -9,10 +9,12 @@
 namespace msim {
 
 void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, std::vector<int64_t>& info,
-                       std::vector<uint64_t>& tiles) {
+                       std::vector<uint64_t>& table, int64_t& stride) {
   info.clear();
-  tiles.clear();
+  table.clear();
+  stride = 0;
   if (n <= 0) return;
+  std::vector<uint64_t> tiles;
   waves = std::max<int64_t>(1, waves);
   constexpr int64_t kMaxWaveTokens = int64_t(1) << 25;  // (T1 - T0) * 64 stays below 2^31
   std::vector<int64_t> cost(n + 1, 0);
@@ -63,6 +65,20 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, std::vector
     for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
     const int64_t row[kWaveInfoWords] = {n, 0, off[n], off[n], 0, tab0, 0, 0};
     info.insert(info.end(), row, row + kWaveInfoWords);
+  }
+  // Every wave's entries at a fixed stride (a multiple of 8 entries, 64 B),
+  // so a wave finds them from its index alone, without reading its row of
+  // `info` first; the rest of a slot is padding.
+  const int64_t nw = (int64_t)info.size() / kWaveInfoWords;
+  int64_t longest = 0;
+  for (int64_t w = 0; w < nw; ++w) longest = std::max<int64_t>(longest, info[w * kWaveInfoWords + 4]);
+  stride = ((longest + kScanPrefetch + 1 + 7) / 8) * 8;
+  table.assign((size_t)(nw * stride), kScanPastEnd);
+  for (int64_t w = 0; w < nw; ++w) {
+    int64_t* row = &info[w * kWaveInfoWords];
+    const int64_t cnt = row[4];
+    std::copy(tiles.begin() + row[5], tiles.begin() + row[5] + cnt, table.begin() + w * stride);
+    row[5] = w * stride;
   }
 }
 

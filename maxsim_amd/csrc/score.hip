@@ -278,14 +278,18 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
       unpack_a_int4_order(cur.a, a0, a1);
     else
       unpack_a(cur.a, a0, a1);
+    // All first halves, then all second halves: consecutive MFMAs are
+    // independent, so the matrix pipe never waits on its own result.
     v4i acc[L][NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int l = 0; l < L; ++l) {
+      for (int l = 0; l < L; ++l)
         acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
-        acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], acc[l][j], 0, 0, 0);
-      }
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int l = 0; l < L; ++l) acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], acc[l][j], 0, 0, 0);
     v4i accr[RES ? L : 1][RES ? NT : 1];
     if constexpr (RES) {
       v4i r0, r1;
@@ -293,10 +297,13 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
 #pragma unroll
       for (int j = 0; j < NT; ++j)
 #pragma unroll
-        for (int l = 0; l < L; ++l) {
+        for (int l = 0; l < L; ++l)
           accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int l = 0; l < L; ++l)
           accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], accr[l][j], 0, 0, 0);
-        }
     }
 
     if constexpr (INTMAX) {
