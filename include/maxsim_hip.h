@@ -46,6 +46,14 @@ int msim_abi_version(void);
  * (cuda_extension.cu:3489-3513), whose SM89 warp shapes have no gfx950 meaning. */
 int msim_set_docs_per_wave(int value);
 int msim_get_docs_per_wave(void);
+/* Top-k selection of the int8-query search: 1 (default) = the scan's
+ * last workgroup selects when the call fits (k <= 32, 256..4096 documents,
+ * <= 8 batch rows per scan pass), 0 = always a separate selection launch,
+ * 2 = fused with the selection's k-round path forced (tests both paths).
+ * No counterpart in the reference, which selects on the host
+ * (cuda_extension.cu:1629-1692 returns full score rows). */
+int msim_set_fused_topk(int mode);
+int msim_get_fused_topk(void);
 
 /* ===================================================================== */
 /* Int4 corpus handle: CudaInt4PackedDocs (cuda_extension.cu:2677-3306). */

@@ -71,6 +71,17 @@ def get_docs_per_wave() -> int:
     return int(_native.load().msim_get_docs_per_wave())
 
 
+def set_fused_topk(mode: int) -> None:
+    """Top-k selection of the int8-query search: 1 = in the scan's last
+    workgroup when the call fits (default), 0 = separate launch, 2 = fused
+    with the k-round selection path forced (testing)."""
+    check(_native.load().msim_set_fused_topk(int(mode)))
+
+
+def get_fused_topk() -> int:
+    return int(_native.load().msim_get_fused_topk())
+
+
 class CudaInt4PackedDocs:
     """Resident int4 corpus (reference: CudaInt4PackedDocs, cu:2677-3306)."""
 

@@ -14,6 +14,7 @@ namespace msim {
 
 thread_local std::string g_last_error;
 int g_docs_per_wave = 0;
+int g_fused_topk = 1;  // msim_set_fused_topk
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -89,6 +90,15 @@ extern "C" int msim_set_docs_per_wave(int value) {
 }
 
 extern "C" int msim_get_docs_per_wave(void) { return g_docs_per_wave; }
+
+extern "C" int msim_set_fused_topk(int mode) {
+  return guarded([&] {
+    if (mode < 0 || mode > 2) throw InvalidArgument("fused top-k mode must be 0, 1 or 2");
+    g_fused_topk = mode;
+  });
+}
+
+extern "C" int msim_get_fused_topk(void) { return g_fused_topk; }
 
 // -------------------------------------------------------------- int4 handle
 
@@ -237,8 +247,26 @@ int64_t scan_waves(const msim_int4_docs* h) {
 
 // Score the query quantised in the workspace: the MFMA scan for passes of at
 // most 128 query rows, the row-maxima path beyond.
+#ifndef MSIM_SCAN_PASS_ROWS
+#define MSIM_SCAN_PASS_ROWS 128
+#endif
+constexpr int64_t kScanPassRows = MSIM_SCAN_PASS_ROWS;  // query rows per scan launch
+
+// The scan selects the top-k itself (last-workgroup tail) when every pass's
+// batch rows and the corpus fit the tail's limits.
+bool scan_fuses_topk(const msim_int4_docs* h, int64_t batch, int64_t query_tokens, int64_t k) {
+  if (g_fused_topk == 0 || k <= 0 || query_tokens == 0 || query_tokens > 128 || h->num_docs == 0) return false;
+  const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
+  return k <= msim::kScanTailMaxK && h->num_docs >= msim::kScanTailMinDocs && h->num_docs <= msim::kScanTailMaxDocs &&
+         std::min(per_pass, batch) <= msim::kScanTailMaxRows;
+}
+
+// Scores of the quantised query against every document into d_scores [B, N];
+// with k > 0 (scan_fuses_topk true) the scores go to the handle's padded
+// tail rows instead (d_scores unused) and the top-k of each batch row to
+// d_top_s / d_top_i [B, k].
 void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* d_scores,
-                     hipStream_t stream) {
+                     hipStream_t stream, int64_t k = 0, float* d_top_s = nullptr, int64_t* d_top_i = nullptr) {
   if (query_tokens == 0 || h->num_docs == 0 || query_tokens > 128) {
     score_int8q(h, batch, query_tokens, d_scores, stream);
     return;
@@ -257,28 +285,56 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
   a.query_tokens = (int32_t)query_tokens;
   a.scale = h->scale;
   a.score_stride = h->num_docs;
-#ifndef MSIM_SCAN_PASS_ROWS
-#define MSIM_SCAN_PASS_ROWS 128
-#endif
-  const int64_t per_pass = std::max<int64_t>(1, MSIM_SCAN_PASS_ROWS / query_tokens);
+  a.num_docs = h->num_docs;
+  if (k > 0) {
+    // Fill kernels, not memsets, so that a captured call records no memset
+    // node; both fills run once per allocation.
+    if (h->ticket.ptr == nullptr) {
+      h->ticket.ensure(256, "hipMalloc scan ticket");
+      check_hip(launch_fill_f32(h->ticket.as<float>(), 1, 0.0f, stream), "zero scan ticket");
+    }
+    if (h->tail_rows < batch) {
+      h->tail_scores.ensure(sizeof(float) * (size_t)(batch * kScanTailRow), "hipMalloc scan tail rows");
+      h->tail_rows = (int64_t)(h->tail_scores.cap / (sizeof(float) * kScanTailRow));
+      float pad;
+      const uint32_t bits = 0xFFFFFFFFu;
+      std::memcpy(&pad, &bits, sizeof pad);
+      check_hip(launch_fill_f32(h->tail_scores.as<float>(), h->tail_rows * kScanTailRow, pad, stream),
+                "fill scan tail rows");
+    }
+    d_scores = h->tail_scores.as<float>();
+    a.score_stride = kScanTailRow;
+    a.topk_k = (int32_t)k;
+    a.tail_cap = g_fused_topk == 2 ? 0 : INT32_MAX;
+    a.ticket = h->ticket.as<uint32_t>();
+  }
+  const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
   for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
     const int64_t nb = std::min(per_pass, batch - b0);
     a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;
     a.qscale = h->qscale.as<float>() + b0 * query_tokens;
     a.batch = (int32_t)nb;
-    a.scores = d_scores + b0 * h->num_docs;
+    a.scores = d_scores + b0 * a.score_stride;
+    if (k > 0) {
+      a.top_scores = d_top_s + b0 * k;
+      a.top_ids = d_top_i + b0 * k;
+    }
     check_hip(launch_int8q_scan(a, h->has_token_scale, stream), "launch int8q scan kernel");
   }
 }
 
 // Full int8-query search: scores of every document into d_scores [B, N] and,
 // when k > 0, the top-k of each batch row into d_top_s / d_top_i [B, k].
-// Quantisation, the scan and the selection are separate launches on one
-// stream.
+// Quantisation and the scan are launches on one stream; the selection is the
+// scan's tail when it fits (scan_fuses_topk), else a launch of its own.
 void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                   float* d_scores, int64_t k, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   if (batch == 0) return;
   quantize_int8q(h, d_query, batch, query_tokens, stream);
+  if (scan_fuses_topk(h, batch, query_tokens, k)) {
+    score_quantized(h, batch, query_tokens, d_scores, stream, k, d_top_s, d_top_i);
+    return;
+  }
   score_quantized(h, batch, query_tokens, d_scores, stream);
   if (k > 0)
     check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, d_top_s, d_top_i, stream),

@@ -95,6 +95,10 @@ struct msim_int4_docs {
   msim::DeviceBuffer codes128, residual128, ones16;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
+  // Scan with fused top-k: workgroup ticket (zero between launches) and score
+  // rows of kScanTailRow floats, prefilled with the padding bits 0xFFFFFFFF.
+  msim::DeviceBuffer ticket, tail_scores;
+  int64_t tail_rows = 0;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
@@ -103,7 +107,7 @@ struct msim_int4_docs {
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap + top_indices.cap +
-           rowmax.cap + wave_info.cap + tile_table.cap + ws.bytes();
+           rowmax.cap + wave_info.cap + tile_table.cap + ticket.cap + tail_scores.cap + ws.bytes();
   }
 };
 

@@ -22,6 +22,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes, kBufferFlags);
 }
 
+// Cache-policy operand of a buffer load that reads the agent-coherent copy
+// (the sc1 bit, as on an agent-scope atomic load).
+constexpr int kCoherentLoadPolicy = 16;
+
 __device__ __forceinline__ v4u load_b128(__amdgpu_buffer_rsrc_t r, int byte_offset) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0);
 }

@@ -27,9 +27,14 @@
 //  * software pipelined: the MFMAs of tile i are issued before the VALU
 //    epilogue (scale, running max) of tile i - 1;
 //  * at a document end: cross-lane max over the four lane groups and numpy's
-//    float64 pairwise sum over query tokens.
+//    float64 pairwise sum over query tokens;
+//  * fused selection (ScanArgs::topk_k > 0): scores are stored write-through
+//    and every workgroup takes a ticket once its stores have completed; the
+//    last one selects each batch row's top-k (topk_block.hpp, tail form),
+//    one wave per row, in its own LDS.
 #include "common.hpp"
 #include "internal.hpp"
+#include "topk_block.hpp"
 
 namespace msim {
 
@@ -37,11 +42,20 @@ constexpr int kScanThreads = 256;
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kPrefetch = kScanPrefetch;  // tiles in flight per wave
 static_assert(kPrefetch >= 2, "ring of at least two tiles");
+static_assert(kScanTailRow == kTailRow && kScanTailMaxDocs <= kTailRow, "fused selection rows");
+static_assert(kScanTailMaxK <= kWave, "fused selection k");
 
 // Maximum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
 __device__ __forceinline__ float max_over_groups(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// A score store; write-through (agent-scope atomic) when the launch selects
+// its top-k from scores written by other workgroups.
+__device__ __forceinline__ void put_score(float* p, float v, bool coherent) {
+  if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
 }
 
 // out[b * stride] = f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale), b < batch.
@@ -50,7 +64,8 @@ __device__ __forceinline__ float max_over_groups(float v) {
 // eight lanes per batch row).  Each path issues at most two global stores.
 static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, const float* qs, int batch,
                                                        int query_tokens, double scale,
-                                                       float* __restrict__ out, int64_t stride) {
+                                                       float* __restrict__ out, int64_t stride,
+                                                       bool coherent) {
   const int lane = lane_id();
   auto prod = [&](int r) -> double { return (double)rowmax[r] * (double)qs[r]; };
   if (query_tokens < 8) {
@@ -60,7 +75,7 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
       double res = 0.0;
       if (b < batch) {
         for (int q = 0; q < query_tokens; ++q) res = __dadd_rn(res, prod(b * query_tokens + q));
-        out[(int64_t)b * stride] = (float)(res * scale);
+        put_score(out + (int64_t)b * stride, (float)(res * scale), coherent);
       }
     }
     return;
@@ -82,7 +97,7 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
     if (k == 0) r = __dadd_rn(r, o);
     if (k == 0 && valid) {
       for (int i = body; i < query_tokens; ++i) r = __dadd_rn(r, prod(base + i));
-      out[(int64_t)b * stride] = (float)(r * scale);
+      put_score(out + (int64_t)b * stride, (float)(r * scale), coherent);
     }
   }
 }
@@ -122,6 +137,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   const int ntiles = (int)info[4];
   const auto tt = as_constant(tile_table) + gw * p.tile_stride;  // no wait on `info`
   const bool has_empty = info[6] != 0;
+  const bool fused = p.topk_k > 0;
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
 
@@ -213,7 +229,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = m[j];
     }
     wave_sync_lds();
-    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride);
+    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride, fused);
     wave_sync_lds();
 #pragma unroll
     for (int j = 0; j < NT; ++j) m[j] = kNegInf;
@@ -323,9 +339,31 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     const int64_t next = ((int64_t)__shfl_down((int)(uint32_t)((uint64_t)off >> 32), 1) << 32) |
                          (uint32_t)__shfl_down((int)(uint32_t)(uint64_t)off, 1);
     if (lane < ndocs && next == off) {
-      for (int b = 0; b < p.batch; ++b) scores[(int64_t)b * p.score_stride + d0 + lane] = 0.0f;
+      for (int b = 0; b < p.batch; ++b) put_score(scores + (int64_t)b * p.score_stride + d0 + lane, 0.0f, fused);
     }
   }
+  if (!fused) return;
+
+  // Fused selection.  Each wave waits until its write-through score stores
+  // have completed, then one thread takes a ticket; the workgroup holding the
+  // last ticket has every score of the launch visible to agent-scope loads.
+  __shared__ uint32_t s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t ticket = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = ticket == gridDim.x - 1 ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_last == 0) return;
+  // Wave w selects batch rows w, w + 4, ...; its tile ring holds the candidates.
+  uint64_t* cand = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
+  constexpr int kCap = (int)(sizeof(s_codes[0]) / sizeof(uint64_t)) - 1;  // and one spare entry
+  for (int b = wave; b < p.batch; b += kScanWaves)
+    tail_topk(scores + (int64_t)b * p.score_stride, p.topk_k, cand, min(kCap, p.tail_cap),
+              p.top_scores + (int64_t)b * p.topk_k,
+              p.top_ids + (int64_t)b * p.topk_k);
+  if (threadIdx.x == 0) __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool kTS>
@@ -351,6 +389,12 @@ static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_
 hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream) {
   const int rows = args.batch * args.query_tokens;
   if (rows <= 0 || rows > 128 || args.num_waves <= 0 || args.num_waves % kScanWaves != 0)
+    return hipErrorInvalidValue;
+  if (args.topk_k > 0 &&
+      (args.topk_k > kScanTailMaxK || args.topk_k > args.num_docs || args.num_docs > kScanTailMaxDocs ||
+       args.num_docs < kScanTailMinDocs || args.score_stride != kTailRow || args.batch > kScanTailMaxRows ||
+       args.ticket == nullptr ||
+       args.top_scores == nullptr || args.top_ids == nullptr))
     return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;

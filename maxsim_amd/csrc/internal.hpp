@@ -79,7 +79,23 @@ struct ScanArgs {
   double scale;                 // tensor scale (1.0 for per-token corpora)
   float* scores;                // [batch, score_stride]
   int64_t score_stride;
+  // Fused selection (topk_k > 0): scores are stored write-through into rows
+  // of score_stride = kScanTailRow floats whose columns num_docs and up hold
+  // the bits 0xFFFFFFFF (kScanTailMinDocs <= num_docs <= kScanTailMaxDocs), and the last
+  // workgroup to take a ticket selects the top-k of every batch row into
+  // top_scores / top_ids [batch, topk_k], then resets *ticket to 0.
+  int32_t topk_k;
+  int32_t tail_cap;             // candidate slots per wave at most (0 forces the k-round path)
+  int64_t num_docs;
+  uint32_t* ticket;             // zero before the launch
+  float* top_scores;
+  int64_t* top_ids;
 };
+constexpr int kScanTailMaxK = 32;
+constexpr int64_t kScanTailMaxDocs = 4096;
+constexpr int64_t kScanTailMinDocs = 256;  // every lane of the selecting wave holds a score
+constexpr int64_t kScanTailRow = 4096;  // floats per score row of the fused selection
+constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
 hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream);
 // Builds the wave table and tile table for `waves` requested waves (the
 // result may hold more rows: ranges are split at kScanMaxDocsPerWave

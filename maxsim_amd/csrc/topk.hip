@@ -29,40 +29,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
 constexpr int kSmallTopkMaxK = 32;
 constexpr int kSmallEPT = 16;
 
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_update_u64(uint64_t old, uint64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)old, (int)(uint32_t)v, CTRL, ROW_MASK, 0xF, false);
-  const uint32_t hi =
-      (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(old >> 32), (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xF, false);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Maximum over the wave, wave-uniform: DPP butterflies and rotations within
-// rows of 16 lanes, row broadcasts 15 and 31 into lane 63, then readlane.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  uint64_t o = dpp_u64<0xB1>(v);  // quad_perm [1,0,3,2]
-  v = v > o ? v : o;
-  o = dpp_u64<0x4E>(v);  // quad_perm [2,3,0,1]
-  v = v > o ? v : o;
-  o = dpp_u64<0x124>(v);  // row_ror:4
-  v = v > o ? v : o;
-  o = dpp_u64<0x128>(v);  // row_ror:8
-  v = v > o ? v : o;
-  o = dpp_update_u64<0x142, 0xA>(v, v);  // row_bcast:15 into rows 1 and 3
-  v = v > o ? v : o;
-  o = dpp_update_u64<0x143, 0xC>(v, v);  // row_bcast:31 into rows 2 and 3
-  v = v > o ? v : o;
-  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63) << 32) |
-         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-}
-
 // Maximum of a 32-bit value over the wave (wave-uniform), DPP only.
 __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
   v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));

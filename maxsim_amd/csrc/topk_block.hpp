@@ -19,10 +19,46 @@
 
 namespace msim {
 
+// Integer operations only, so the key of every bit pattern (NaNs included)
+// is independent of floating-point compile flags.
 __device__ __forceinline__ uint32_t score_key(float s) {
-  if (s == 0.0f) s = 0.0f;
-  const uint32_t u = __float_as_uint(s);
+  uint32_t u = __float_as_uint(s);
+  if (u == 0x80000000u) u = 0u;  // -0 ties +0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_update_u64(uint64_t old, uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)old, (int)(uint32_t)v, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(old >> 32), (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xF, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Maximum over the wave, wave-uniform: DPP butterflies and rotations within
+// rows of 16 lanes, row broadcasts 15 and 31 into lane 63, then readlane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  uint64_t o = dpp_u64<0xB1>(v);  // quad_perm [1,0,3,2]
+  v = v > o ? v : o;
+  o = dpp_u64<0x4E>(v);  // quad_perm [2,3,0,1]
+  v = v > o ? v : o;
+  o = dpp_u64<0x124>(v);  // row_ror:4
+  v = v > o ? v : o;
+  o = dpp_u64<0x128>(v);  // row_ror:8
+  v = v > o ? v : o;
+  o = dpp_update_u64<0x142, 0xA>(v, v);  // row_bcast:15 into rows 1 and 3
+  v = v > o ? v : o;
+  o = dpp_update_u64<0x143, 0xC>(v, v);  // row_bcast:31 into rows 2 and 3
+  v = v > o ? v : o;
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -364,6 +400,142 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
   wave_sync_lds();
   rank_and_write<false>(skey, spos, k, lane, kWave, row, n, id_map, out_scores, out_ids);
   wave_sync_lds();
+}
+
+// ----------------------------------------------------------------- tail form
+// One wave selects the top-k of a row of n <= kTailRow scores that other
+// workgroups of the same launch wrote with agent-scope atomic stores; they are
+// read back with coherent loads.  The row occupies kTailRow floats, positions
+// n and up holding the padding bits 0xFFFFFFFF: their keys are 0, the lowest,
+// and their positions are above every score's, so padding ranks below every
+// score and, as k <= n, is never selected; no element needs a bounds check.
+// With T32 the k-th largest of the lanes' maximum 32-bit keys, every key of
+// the top-k is >= T32 and those candidates lie in the (about k) lanes whose
+// maximum reaches T32.  They go to `cand` (wave-private LDS of at least
+// cap + 1 entries) with their 64-bit keys (order-preserving score bits above
+// the inverted position, unique) and are ranked by counting.  More than
+// `cap` candidates (the best scores crowded into few lanes, or many ties;
+// cap = 0 forces it) fall back to k rounds of a wave maximum over the row.
+// 1 <= k <= 64, 256 <= n (every lane's maximum is a score's, not padding).
+constexpr int kTailEPT = 64;
+constexpr int kTailRow = kTailEPT * kWave;  // 4096
+constexpr uint32_t kTailPadBits = 0xFFFFFFFFu;
+
+__device__ __forceinline__ uint64_t full_key(uint32_t key, uint32_t pos) {
+  return ((uint64_t)key << 32) | (0xFFFFFFFFu - pos);
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int src) {
+  return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), src) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
+}
+
+// Position of register element e of a lane: 16-byte loads of 4 scores, load
+// e / 4 of lane l covering positions 4 (64 (e / 4) + l) .. + 3.
+__device__ __forceinline__ uint32_t tail_pos(int e, int lane) {
+  return (uint32_t)(4 * ((e >> 2) * kWave + lane) + (e & 3));
+}
+
+// Loads carry the agent-scope coherence bit (sc1), as an agent-scope atomic
+// load does.
+__device__ __forceinline__ v4u tail_load(__amdgpu_buffer_rsrc_t rs, int e4, int lane) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rs, (e4 * kWave + lane) * 16, 0, kCoherentLoadPolicy);
+}
+
+// The score of a key (+0 and -0 share one: read back from the row).
+__device__ __forceinline__ void tail_write(uint64_t key, const float* row, float* out_s, int64_t* out_i) {
+  const uint32_t k32 = (uint32_t)(key >> 32);
+  const uint32_t pos = 0xFFFFFFFFu - (uint32_t)key;
+  float s = __uint_as_float((k32 & 0x80000000u) ? (k32 & 0x7FFFFFFFu) : ~k32);
+  if (k32 == 0x80000000u) s = load_score<true>(row + pos);
+  *out_s = s;
+  *out_i = (int64_t)pos;
+}
+
+// Not inlined: the caller's registers are free by then, and inlining would
+// let the register allocation of a large caller grow around it.  Arguments
+// arrive in VGPRs; the wave-uniform ones are moved back to SGPRs.
+__device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int k_arg, uint64_t* cand_arg, int cap_arg,
+                                                    float* out_s_arg, int64_t* out_i_arg) {
+  const float* row = reinterpret_cast<const float*>(wave_uniform64(reinterpret_cast<int64_t>(row_arg)));
+  float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
+  int64_t* out_i = reinterpret_cast<int64_t*>(wave_uniform64(reinterpret_cast<int64_t>(out_i_arg)));
+  const int k = wave_uniform(k_arg), cap = wave_uniform(cap_arg);
+  // `cand_arg` points into LDS: address it as LDS (ds_* instructions).
+  typedef __attribute__((address_space(3))) uint64_t lds_u64;
+  lds_u64* cand = (lds_u64*)cand_arg;
+  const int lane = lane_id();
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(row, (uint32_t)kTailRow * 4u);
+  uint32_t key[kTailEPT];
+#pragma unroll
+  for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
+    const v4u v = tail_load(rs, e4, lane);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) key[4 * e4 + c] = score_key(__uint_as_float(v[c]));
+  }
+  // T32, the k-th largest of the 64 lanes' maximum keys (ties counted), is
+  // at most the row's k-th largest key: the lanes holding the k largest
+  // maxima hold k keys >= T32.  Every key >= T32 is a candidate.
+  uint32_t mkey = 0;
+#pragma unroll
+  for (int e = 0; e < kTailEPT; ++e) mkey = max(mkey, key[e]);
+  int above = 0;  // lane maxima above this lane's (readlane: no LDS round trips)
+#pragma unroll 4
+  for (int j = 0; j < kWave; ++j) above += (uint32_t)__builtin_amdgcn_readlane((int)mkey, j) > mkey ? 1 : 0;
+  const uint32_t t32 = wave_min_u32(above < k ? mkey : 0xFFFFFFFFu);
+
+  int cnt = 0;
+#pragma unroll
+  for (int e = 0; e < kTailEPT; ++e) cnt += key[e] >= t32 ? 1 : 0;
+  const int incl = (int)wave_inclusive_scan((uint32_t)cnt);
+  const int total = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= k
+  if (total <= cap) {
+    // Unconditional stores: a non-candidate goes to the spare entry `cap`.
+    int slot = incl - cnt;
+    if (cnt > 0) {
+#pragma unroll
+      for (int e = 0; e < kTailEPT; ++e) {
+        const bool take = key[e] >= t32;
+        cand[take ? slot : cap] = full_key(key[e], tail_pos(e, lane));
+        slot += take ? 1 : 0;
+      }
+    }
+    wave_sync_lds();
+    if (total <= kWave) {
+      // One candidate per lane, ranked by readlane.
+      const uint64_t x = lane < total ? (uint64_t)cand[lane] : 0ull;
+      int r = 0;
+#pragma unroll 4
+      for (int j = 0; j < total; ++j) r += readlane_u64(x, j) > x ? 1 : 0;
+      if (lane < total && r < k) tail_write(x, row, out_s + r, out_i + r);
+    } else {
+      for (int s = lane; s < total; s += kWave) {
+        const uint64_t x = cand[s];
+        int r = 0;
+        for (int t = 0; t < total; ++t) r += cand[t] > x ? 1 : 0;
+        if (r < k) tail_write(x, row, out_s + r, out_i + r);
+      }
+    }
+    wave_sync_lds();
+    return;
+  }
+  // k rounds over the row: the largest key below the previous round's.
+  uint64_t prev = ~0ull;
+  for (int r = 0; r < k; ++r) {
+    uint64_t best = 0;
+#pragma unroll 1
+    for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
+      const v4u v = tail_load(rs, e4, lane);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint64_t f = full_key(score_key(__uint_as_float(v[c])), tail_pos(4 * e4 + c, lane));
+        best = (f < prev && f > best) ? f : best;
+      }
+    }
+    const uint64_t top = wave_max_u64(best);
+    if (lane == 0) tail_write(top, row, out_s + r, out_i + r);
+    prev = top;
+  }
 }
 
 }  // namespace msim

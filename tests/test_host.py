@@ -59,6 +59,14 @@ def test_docs_per_wave_knob_validation():
     assert lib.msim_get_docs_per_wave() == 0
 
 
+def test_fused_topk_knob_validation():
+    lib = _native.load()
+    assert lib.msim_set_fused_topk(3) == _native.MSIM_EINVAL
+    assert b"fused top-k mode" in lib.msim_last_error()
+    assert lib.msim_get_fused_topk() == 1
+    assert lib.msim_set_fused_topk(1) == _native.MSIM_OK
+
+
 def test_product_never_imports_the_oracle():
     """The checker lives in oracle/; nothing under maxsim_amd/ may load it."""
     pkg = os.path.join(ROOT, "maxsim_amd")
