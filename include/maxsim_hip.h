@@ -122,6 +122,11 @@ int msim_int4_quantize_int8q_async(msim_int4_docs* h, const float* d_query, int6
                                    int64_t query_tokens, void* stream);
 int msim_int4_score_int8q_async(msim_int4_docs* h, int64_t batch, int64_t query_tokens,
                                 float* d_out, void* stream);
+/* Top-k [batch, k] of the last quantised query: the scan with its fused
+ * selection when the call fits (see msim_set_fused_topk), else the scan and a
+ * selection launch; the second half of msim_int4_topk_int8q_async. */
+int msim_int4_topk_quantized_async(msim_int4_docs* h, int64_t batch, int64_t query_tokens, int64_t k,
+                                   float* d_scores, int64_t* d_indices, void* stream);
 /* Top-k of device score rows d_scores[b * row_stride + i], i < n, ordered by
  * (score desc, position asc); the block selector of topk_kernel (cu:1629-1692). */
 int msim_topk_async(const float* d_scores, int64_t batch, int64_t n, int64_t row_stride,

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, list] = {
     "msim_int4_topk_int8q_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
     "msim_int4_quantize_int8q_async": [c_vp, c_vp, c_i64, c_i64, c_vp],
     "msim_int4_score_int8q_async": [c_vp, c_i64, c_i64, c_vp, c_vp],
+    "msim_int4_topk_quantized_async": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
     "msim_topk_async": [c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
     "msim_int4_maxsim_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp],
     "msim_int4_topk_batch": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],

@@ -327,10 +327,19 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
 // when k > 0, the top-k of each batch row into d_top_s / d_top_i [B, k].
 // Quantisation and the scan are launches on one stream; the selection is the
 // scan's tail when it fits (scan_fuses_topk), else a launch of its own.
+void select_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* d_scores, int64_t k,
+                      float* d_top_s, int64_t* d_top_i, hipStream_t stream);
+
 void search_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                   float* d_scores, int64_t k, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   if (batch == 0) return;
   quantize_int8q(h, d_query, batch, query_tokens, stream);
+  select_quantized(h, batch, query_tokens, d_scores, k, d_top_s, d_top_i, stream);
+}
+
+// Scores (and with k > 0 the top-k) of the last quantised query.
+void select_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* d_scores, int64_t k,
+                      float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   if (scan_fuses_topk(h, batch, query_tokens, k)) {
     score_quantized(h, batch, query_tokens, d_scores, stream, k, d_top_s, d_top_i);
     return;
@@ -561,6 +570,22 @@ extern "C" int msim_int4_score_int8q_async(msim_int4_docs* h, int64_t batch, int
     if (batch == 0 || h->num_docs == 0) return;
     select_device(h->device);
     score_quantized(h, batch, query_tokens, d_out, as_stream(stream));
+  });
+}
+
+extern "C" int msim_int4_topk_quantized_async(msim_int4_docs* h, int64_t batch, int64_t query_tokens, int64_t k,
+                                              float* d_scores, int64_t* d_indices, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    check_k(k, h->num_docs);
+    check_int8q(h);
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    if (h->quantized_rows != batch * query_tokens)
+      throw InvalidArgument("no quantised query of this shape: call quantize first with the same batch and query_tokens");
+    select_device(h->device);
+    float* d_full = ensure_scores(h, batch, h->num_docs);
+    select_quantized(h, batch, query_tokens, d_full, k, d_scores, d_indices, as_stream(stream));
   });
 }
 

@@ -108,7 +108,7 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
 #define MSIM_SCAN_OCCUPANCY
 #endif
 
-template <int NT, bool kTS>
+template <int NT, bool kTS, bool kTail>
 __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_kernel(
     ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale16,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   const int ntiles = (int)info[4];
   const auto tt = as_constant(tile_table) + gw * p.tile_stride;  // no wait on `info`
   const bool has_empty = info[6] != 0;
-  const bool fused = p.topk_k > 0;
+  constexpr bool fused = kTail;  // p.topk_k > 0 exactly when kTail
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
 
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       for (int b = 0; b < p.batch; ++b) put_score(scores + (int64_t)b * p.score_stride + d0 + lane, 0.0f, fused);
     }
   }
-  if (!fused) return;
+  if constexpr (!fused) return;
 
   // Fused selection.  Each wave waits until its write-through score stores
   // have completed, then one thread takes a ticket; the workgroup holding the
@@ -366,12 +366,12 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (threadIdx.x == 0) __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool kTS>
+template <bool kTS, bool kTail>
 static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_t stream) {
   const dim3 grid((unsigned)blocks), block(kScanThreads);
   switch (nt) {
 #define MSIM_SCAN_CASE(N)                                                                           \
-  int8q_scan_kernel<N, kTS><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
+  int8q_scan_kernel<N, kTS, kTail><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
                                                         a.wave_info, a.tile_table, a.qpack, a.qscale, \
                                                         a.scores)
     case 1: MSIM_SCAN_CASE(1); break;
@@ -398,8 +398,14 @@ hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t
     return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;
-  if (token_scale) launch_scan_nt<true>(args, nt, blocks, stream);
-  else launch_scan_nt<false>(args, nt, blocks, stream);
+  const bool tail = args.topk_k > 0;
+  if (token_scale) {
+    if (tail) launch_scan_nt<true, true>(args, nt, blocks, stream);
+    else launch_scan_nt<true, false>(args, nt, blocks, stream);
+  } else {
+    if (tail) launch_scan_nt<false, true>(args, nt, blocks, stream);
+    else launch_scan_nt<false, false>(args, nt, blocks, stream);
+  }
   return hipGetLastError();
 }
 
