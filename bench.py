@@ -25,6 +25,7 @@ HBM bytes per scan launch.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import csv
 import json
 import os
@@ -56,6 +57,8 @@ def parse_args():
     ap.add_argument("--docs-per-wave", type=int, default=0)
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="append plain device copies of known size (PMC calibration)")
+    ap.add_argument("--pack", action="store_true",
+                    help="measure the device int4 packer (index build) instead of a search config")
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="BASELINE configuration to measure (2 = the headline metric)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -596,6 +599,66 @@ def bench_config5(args):
                     "bytes_per_token": 88, "cpu_baseline": None})
 
 
+def bench_pack(args):
+    """Index build: the config-2 corpus (fp32 [T,128], 268 MB) packed to
+    per-token int4 on the device (msim_pack_int4_async, values array off).
+    One step = one pack of the whole corpus, device-resident; HBM roofline
+    from 512 B read + 64 B codes + 4 B scale written per token.  The host
+    packer (NumPy, the reference's pack_int4_symmetric) is timed beside it."""
+    import torch
+
+    from maxsim_amd import _native, synthetic
+    from maxsim_amd.experimental import pack_int4_symmetric, pack_int4_symmetric_device
+
+    cfg = synthetic.CONFIGS[2]
+    corpus = synthetic.make_corpus(cfg["num_docs"], cfg["lo"], cfg["hi"])
+    x_np = np.ascontiguousarray(corpus.embeddings, np.float32)
+    t, d = x_np.shape
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x = torch.from_numpy(x_np).to(dev)
+    codes = torch.empty((t, d // 2), dtype=torch.uint8, device=dev)
+    tscale = torch.empty((t,), dtype=torch.float32, device=dev)
+    work = torch.zeros(2, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    lib = _native.load()
+
+    def step():
+        _native.check(lib.msim_pack_int4_async(_native.ptr(x), t, d, 1, 0.0, _native.ptr(codes), _native.ptr(tscale),
+                                               None, _native.ptr(work), sptr))
+
+    host = pack_int4_symmetric(x_np, corpus.offsets, scale_granularity="token")
+    step()
+    torch.cuda.synchronize()
+    assert np.array_equal(codes.cpu().numpy(), host.data), "device pack differs from the host packer"
+    assert np.array_equal(tscale.cpu().numpy().view(np.uint32), host.token_scale.view(np.uint32))
+    ms, ev = _timed(step, args.steps, args.warmup, stream)
+    nbytes = t * (4 * d + d // 2 + 4)
+    achieved = nbytes / (float(np.mean(ev)) * 1e-3) / 1e9
+    h0 = time.perf_counter()
+    pack_int4_symmetric(x_np, corpus.offsets, scale_granularity="token")
+    host_s = time.perf_counter() - h0
+    api0 = time.perf_counter()
+    pack_int4_symmetric_device(x_np, corpus.offsets, scale_granularity="token")
+    api_s = time.perf_counter() - api0
+    tensor0 = time.perf_counter()
+    tensor = pack_int4_symmetric_device(x, corpus.offsets, scale_granularity="tensor", values=False)
+    tensor_s = time.perf_counter() - tensor0
+    assert np.array_equal(tensor.data, pack_int4_symmetric(x_np, scale_granularity="tensor").data)
+    return _result("tokens packed/sec, per-token int4 index build on the device (1 GPU)", t / (ms * 1e-3),
+                   "tokens/s", args, ms, float(np.percentile(ev, 50)), float(np.percentile(ev, 95)), "f32->int4",
+                   f"config-2 corpus: {t} tokens x {d} fp32 -> int4 codes + token scales",
+                   {"roofline": {"kernel": "pack_int4_dim128_kernel<true>", "bound": "hbm", "achieved": achieved,
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                                 "traffic": None, "algorithmic_bytes_per_launch": nbytes},
+                    "host_numpy_pack_s": host_s,
+                    "api_sync_pack_s_including_transfers": api_s,
+                    "tensor_scale_device_pack_s": tensor_s,
+                    "cpu_baseline": {"value": t / host_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+                                     "sample": "one NumPy pack_int4_symmetric of the whole corpus"}})
+
+
 OTHER_CONFIGS = {3: bench_config3, 4: bench_config4, 5: bench_config5}
 
 
@@ -609,7 +672,9 @@ def main():
               "scores on a single MI355X (the sharding design is written up in DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.config == 2:
+    if args.pack:
+        print(json.dumps(bench_pack(args)), flush=True)
+    elif args.config == 2:
         bench_config2(args)
     else:
         print(json.dumps(OTHER_CONFIGS[args.config](args)), flush=True)

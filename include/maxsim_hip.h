@@ -55,6 +55,24 @@ int msim_get_docs_per_wave(void);
 int msim_set_fused_topk(int mode);
 int msim_get_fused_topk(void);
 
+/* Symmetric int4 packing on the device: pack_int4_symmetric
+ * (experimental.py:218-268) with codes in _pack_signed_int4_values' nibble
+ * order (experimental.py:604-609), bit-identical to the host packer.
+ * token_granularity 1 = "token" (per-token scales into token_scales[T]),
+ * 0 = "tensor"; scale 0 means None (tensor: max|x| / 7).  values [T, dim]
+ * int8 is optional (NULL).  The reference's argument checks and messages.
+ *
+ * Host arrays in and out (uploads, packs, downloads; *scale_out receives the
+ * tensor scale, 1.0 for token granularity): */
+int msim_pack_int4(const float* x, int64_t num_tokens, int dim, int token_granularity, double scale,
+                   uint8_t* codes, float* token_scales, int8_t* values, double* scale_out);
+/* Device arrays (x 16-byte aligned), enqueued on `stream`; work = 2 device
+ * words: work[0] receives max|x| bits (tensor granularity), work[1] != 0 when
+ * x holds a non-finite value (the caller checks it after the stream). */
+int msim_pack_int4_async(const float* d_x, int64_t num_tokens, int dim, int token_granularity, double scale,
+                         uint8_t* d_codes, float* d_token_scales, int8_t* d_values, uint32_t* d_work,
+                         void* stream);
+
 /* ===================================================================== */
 /* Int4 corpus handle: CudaInt4PackedDocs (cuda_extension.cu:2677-3306). */
 /* ===================================================================== */

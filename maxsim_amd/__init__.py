@@ -28,6 +28,7 @@ from maxsim_amd.experimental import (
     int4_maxsim_int8q,
     int4_to_device,
     pack_int4_symmetric,
+    pack_int4_symmetric_device,
     topk_int4_maxsim,
 )
 
@@ -57,6 +58,7 @@ __all__ = [
     "int4_to_device",
     "maxsim",
     "pack_int4_symmetric",
+    "pack_int4_symmetric_device",
     "pack_query_signs",
     "pack_signs",
     "score",

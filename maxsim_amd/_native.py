@@ -27,6 +27,8 @@ SIGNATURES: dict[str, list] = {
     "msim_set_docs_per_wave": [c_int],
     "msim_get_docs_per_wave": [],
     "msim_set_fused_topk": [c_int],
+    "msim_pack_int4": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp],
+    "msim_pack_int4_async": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp, c_vp],
     "msim_get_fused_topk": [],
     # int4 handle
     "msim_int4_create": [c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_dbl, c_vp],

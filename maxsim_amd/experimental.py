@@ -1,12 +1,14 @@
 """Int4 corpus format and int4 scoring dispatch (reference: src/maxsim/experimental.py).
 
-Packing is host NumPy (offline index build, as in the reference).  Scoring
+Packing is host NumPy (offline index build, as in the reference), with a GPU
+packer beside it (``pack_int4_symmetric_device``, same result).  Scoring
 always runs on the GPU: CPU-resident packed docs are uploaded to a device
 handle first; ``device="cpu"`` is rejected because this engine has no CPU
 scoring path.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import numpy as np
@@ -105,6 +107,88 @@ def pack_int4_symmetric(doc_embeddings, doc_offsets=None, *, scale: float | None
         values=np.ascontiguousarray(values),
         doc_offsets=offsets,
         dim=int(docs.shape[1]),
+        num_docs=int(offsets.shape[0] - 1),
+        scale=scale_value,
+        device="cpu",
+        token_scale=token_scale,
+    )
+
+
+def pack_int4_symmetric_device(doc_embeddings, doc_offsets=None, *, scale: float | None = None,
+                               scale_granularity: str = "tensor", values: bool = True) -> Int4PackedDocs:
+    """pack_int4_symmetric on the GPU (msim_pack_int4 / msim_pack_int4_async):
+    the same arguments, checks, messages and result, bit for bit, for a fast
+    index build.  A torch CUDA tensor is packed in place on its device (no
+    host copy of the embeddings); other inputs are uploaded.  ``values=False``
+    skips the int8 values array (``values`` is then None).
+    """
+    from maxsim_amd import _native
+
+    granularity = {"tensor": 0, "token": 1}.get(scale_granularity, -1)
+    scale_arg = 0.0 if scale is None else float(scale)
+    if scale is not None and scale_arg == 0.0:
+        scale_arg = -1.0  # an explicit 0 is invalid (0 means None in the C ABI)
+    lib = _native.load()
+    is_cuda = getattr(doc_embeddings, "is_cuda", False)
+    if is_cuda:
+        import torch
+
+        x = doc_embeddings.detach()
+        if x.ndim != 2:
+            raise ValueError("doc_embeddings must have shape [num_doc_tokens, dim]")
+        x = x.to(torch.float32).contiguous()
+        t, d = int(x.shape[0]), int(x.shape[1])
+        if d <= 0:
+            raise ValueError("dim must be positive")
+        if d % 2 != 0:
+            raise ValueError("dim must be divisible by 2 for int4 packing")
+        if d % 8 != 0:
+            raise ValueError("dim must be divisible by 8")
+        codes = torch.empty((t, d // 2), dtype=torch.uint8, device=x.device)
+        tscale = torch.empty((t,), dtype=torch.float32, device=x.device)
+        vals = torch.empty((t, d), dtype=torch.int8, device=x.device) if values else None
+        work = torch.zeros(2, dtype=torch.int32, device=x.device)
+        if granularity not in (0, 1) or (granularity == 1 and scale is not None) or \
+                (granularity == 0 and scale is not None and not (np.isfinite(scale_arg) and scale_arg > 0.0)):
+            # Finiteness is checked first, as the host packer does.
+            if not bool(torch.isfinite(x).all()):
+                raise ValueError("doc_embeddings must contain only finite values")
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        with torch.cuda.device(x.device):
+            _native.check(lib.msim_pack_int4_async(_native.ptr(x), t, d, granularity, scale_arg, _native.ptr(codes),
+                                                   _native.ptr(tscale), _native.ptr(vals), _native.ptr(work),
+                                                   ctypes.c_void_p(stream)))
+            w = work.cpu().numpy().view(np.uint32)
+        if w[1] != 0:
+            raise ValueError("doc_embeddings must contain only finite values")
+        if granularity == 1:
+            scale_value = 1.0
+        elif scale is not None:
+            scale_value = scale_arg
+        else:
+            peak = float(w[:1].view(np.float32)[0])
+            scale_value = 1.0 if peak == 0.0 else peak / 7.0
+        data = codes.cpu().numpy()
+        token_scale = tscale.cpu().numpy() if granularity == 1 else None
+        values_np = vals.cpu().numpy() if vals is not None else None
+    else:
+        docs = np.ascontiguousarray(_as_numpy(doc_embeddings), dtype=np.float32)
+        if docs.ndim != 2:
+            raise ValueError("doc_embeddings must have shape [num_doc_tokens, dim]")
+        t, d = int(docs.shape[0]), int(docs.shape[1])
+        data = np.empty((t, max(d, 0) // 2), np.uint8)
+        token_scale = np.empty((t,), np.float32) if scale_granularity == "token" else None
+        values_np = np.empty((t, d), np.int8) if values else None
+        out_scale = ctypes.c_double(0.0)
+        _native.check(lib.msim_pack_int4(_native.ptr(docs), t, d, granularity, scale_arg, _native.ptr(data),
+                                         _native.ptr(token_scale), _native.ptr(values_np), ctypes.byref(out_scale)))
+        scale_value = float(out_scale.value)
+    offsets = _normalize_offsets(doc_offsets, t)
+    return Int4PackedDocs(
+        data=data,
+        values=values_np,
+        doc_offsets=offsets,
+        dim=d,
         num_docs=int(offsets.shape[0] - 1),
         scale=scale_value,
         device="cpu",

@@ -67,6 +67,18 @@ def test_fused_topk_knob_validation():
     assert lib.msim_set_fused_topk(1) == _native.MSIM_OK
 
 
+def test_pack_int4_shape_errors_without_device():
+    """Shape checks of the device packer run before any device call
+    (messages of experimental.py:226-232)."""
+    lib = _native.load()
+    assert lib.msim_pack_int4(None, 4, 12, 0, 0.0, None, None, None, None) == _native.MSIM_EINVAL
+    assert b"divisible by 8" in lib.msim_last_error()
+    assert lib.msim_pack_int4(None, 4, 7, 0, 0.0, None, None, None, None) == _native.MSIM_EINVAL
+    assert b"divisible by 2" in lib.msim_last_error()
+    assert lib.msim_pack_int4_async(None, 4, 0, 1, 0.0, None, None, None, None, None) == _native.MSIM_EINVAL
+    assert b"dim must be positive" in lib.msim_last_error()
+
+
 def test_product_never_imports_the_oracle():
     """The checker lives in oracle/; nothing under maxsim_amd/ may load it."""
     pkg = os.path.join(ROOT, "maxsim_amd")
