@@ -409,7 +409,8 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // n and up holding the padding bits 0xFFFFFFFF: their keys are 0, the lowest,
 // and their positions are above every score's, so padding ranks below every
 // score and, as k <= n, is never selected; no element needs a bounds check.
-// With T32 the k-th largest of the lanes' maximum 32-bit keys, every key of
+// With T32 the k-th largest of the lanes' maximum 32-bit keys (ties counted;
+// a radix selection by ballots), every key of
 // the top-k is >= T32 and those candidates lie in the (about k) lanes whose
 // maximum reaches T32.  They go to `cand` (wave-private LDS of at least
 // cap + 1 entries) with their 64-bit keys (order-preserving score bits above
@@ -479,25 +480,42 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int k_
   uint32_t mkey = 0;
 #pragma unroll
   for (int e = 0; e < kTailEPT; ++e) mkey = max(mkey, key[e]);
-  int above = 0;  // lane maxima above this lane's (readlane: no LDS round trips)
-#pragma unroll 4
-  for (int j = 0; j < kWave; ++j) above += (uint32_t)__builtin_amdgcn_readlane((int)mkey, j) > mkey ? 1 : 0;
-  const uint32_t t32 = wave_min_u32(above < k ? mkey : 0xFFFFFFFFu);
+  // Radix selection over the 64 lane maxima, one bit per step from the top:
+  // the k-th largest has bit b set iff at least `need` of the lanes matching
+  // the bits chosen so far have it set (ballot + popcount, no LDS).
+  uint32_t t32 = 0, fixed = 0;
+  int need = k;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t bit = 1u << b;
+    const bool match = (mkey & fixed) == t32;
+    const int ones = __builtin_popcountll(__ballot(match && (mkey & bit) != 0));
+    if (ones >= need) t32 |= bit;
+    else need -= ones;
+    fixed |= bit;
+  }
 
-  int cnt = 0;
+  // Candidate bitmask of the lane (bit e: key[e] >= t32); a candidate's slot
+  // is the lane's base plus the candidates before it, so the stores do not
+  // depend on each other.
+  uint32_t mlo = 0, mhi = 0;
 #pragma unroll
-  for (int e = 0; e < kTailEPT; ++e) cnt += key[e] >= t32 ? 1 : 0;
+  for (int e = 0; e < kTailEPT; ++e) {
+    if (e < 32) mlo |= key[e] >= t32 ? 1u << e : 0u;
+    else mhi |= key[e] >= t32 ? 1u << (e - 32) : 0u;
+  }
+  const int cnt = __builtin_popcount(mlo) + __builtin_popcount(mhi);
   const int incl = (int)wave_inclusive_scan((uint32_t)cnt);
   const int total = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= k
   if (total <= cap) {
     // Unconditional stores: a non-candidate goes to the spare entry `cap`.
-    int slot = incl - cnt;
+    const int base = incl - cnt;
     if (cnt > 0) {
 #pragma unroll
       for (int e = 0; e < kTailEPT; ++e) {
-        const bool take = key[e] >= t32;
-        cand[take ? slot : cap] = full_key(key[e], tail_pos(e, lane));
-        slot += take ? 1 : 0;
+        const bool take = e < 32 ? ((mlo >> e) & 1u) != 0 : ((mhi >> (e - 32)) & 1u) != 0;
+        const int before = e < 32 ? __builtin_popcount(mlo & ((1u << e) - 1u))
+                                  : __builtin_popcount(mlo) + __builtin_popcount(mhi & ((1u << (e - 32)) - 1u));
+        cand[take ? base + before : cap] = full_key(key[e], tail_pos(e, lane));
       }
     }
     wave_sync_lds();
