@@ -24,8 +24,8 @@
 //    byte's nibbles masked in place as int8 (hi = w & 0xF0, lo = (w << 4) &
 //    0xF0), i.e. sixteen times the signed value, so acc = 16 * dot and
 //    float(acc) * (s_t / 16) rounds the same real number as float(dot) * s_t;
-//  * software pipelined: the MFMAs of tile i are issued before the VALU
-//    epilogue (scale, running max) of tile i - 1;
+//  * per tile: 16 MFMAs, then the VALU epilogue (scale, running max); the
+//    two waves of a SIMD overlap one's MFMAs with the other's VALU work;
 //  * at a document end: cross-lane max over the four lane groups and numpy's
 //    float64 pairwise sum over query tokens;
 //  * fused selection (ScanArgs::topk_k > 0): scores are stored write-through
@@ -203,19 +203,19 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   float m[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) m[j] = kNegInf;
-  v4i acc[2][NT];
-  float sc[2][4];
+  v4i acc[NT];
+  float sc[4];
   constexpr float kInf = __builtin_huge_valf();
 
-  // Epilogue of the tile in acc[par] / sc[par]: running max per query row.
-  // A masked row has acc = -2^30 + 16 * dot < 0 and scale +inf, i.e. -inf.
-  auto epilogue_max = [&](int par) {
+  // Epilogue of the tile in acc / sc: running max per query row.  A masked
+  // row has acc = -2^30 + 16 * dot < 0 and scale +inf, i.e. -inf.
+  auto epilogue_max = [&]() {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const float x0 = (float)acc[par][j][0] * sc[par][0];
-      const float x1 = (float)acc[par][j][1] * sc[par][1];
-      const float x2 = (float)acc[par][j][2] * sc[par][2];
-      const float x3 = (float)acc[par][j][3] * sc[par][3];
+      const float x0 = (float)acc[j][0] * sc[0];
+      const float x1 = (float)acc[j][1] * sc[1];
+      const float x2 = (float)acc[j][2] * sc[2];
+      const float x3 = (float)acc[j][3] * sc[3];
       m[j] = max3_op(max3_op(m[j], x0, x1), x2, x3);
     }
   };
@@ -239,15 +239,14 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // tile in `w`, `iss` is the start of the tile kPrefetch steps ahead.
   uint64_t meta = tt[0], iss = tt[kPrefetch];
   int slot = 0;
-  int pv_local = 0;
-  bool pv_last = false;
 
-  // One pipeline step for tile i (in `w`, ring slot `slot`): refill of that
-  // slot, read-back of the next tile, then the tile's MFMAs interleaved with
-  // the epilogue of the previous tile (accumulator set par ^ 1).  Only two
-  // copies of the step are unrolled (the ring slot is a runtime value) to
-  // keep the loop within the instruction cache.
-  auto step = [&](int i, int par, bool has_prev) {
+  // One step for tile i (in `w`, ring slot `slot`): refill of that slot,
+  // read-back of the next tile, the tile's MFMAs and its epilogue.  (A
+  // double-buffered accumulator set, MFMAs of tile i interleaved with the
+  // epilogue of tile i - 1, measured slower: the other wave of the SIMD
+  // already overlaps one wave's MFMAs with another's VALU work, and the
+  // second set costs 64 VGPRs.)
+  auto step = [&](int i) {
     v4i lo, hi;
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
@@ -278,10 +277,10 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       s2 = r0 + 2u < rows ? s2 : kInf;
       s3 = r0 + 3u < rows ? s3 : kInf;
     }
-    sc[par][0] = s0;
-    sc[par][1] = s1;
-    sc[par][2] = s2;
-    sc[par][3] = s3;
+    sc[0] = s0;
+    sc[1] = s1;
+    sc[2] = s2;
+    sc[3] = s3;
     // The slot's contents are in registers before the refill may land.
     lds_read_done(w, sv);
     load_tile(slot, (uint32_t)iss);
@@ -294,42 +293,18 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     // All first halves, then all second halves: consecutive MFMAs are
     // independent, so the matrix pipe never waits on its own result.
 #pragma unroll
-    for (int j = 0; j < NT; ++j) acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+    for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
-      acc[par][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc[par][j], 0, 0, 0);
-    if (has_prev) {
-      epilogue_max(par ^ 1);
-      // One MFMA, then five VALU instructions of the previous tile's epilogue.
-#pragma unroll
-      for (int j = 0; j < 2 * NT; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-      }
-      if (pv_last) finish(pv_local);
-    }
-    pv_last = last;
-    pv_local = local;
+    for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc[j], 0, 0, 0);
+    epilogue_max();
+    if (last) finish(local);
     meta = meta_n;
     iss = iss_n;
   };
 
-  if (ntiles > 0) {
-    // Tile i lives in ring slot i % kPrefetch and accumulator set i & 1.
-    step(0, 0, false);
-    int i = 1;
-    for (; i + 2 <= ntiles; i += 2) {
-      step(i, 1, true);
-      step(i + 1, 0, true);
-    }
-    if (i < ntiles) {
-      step(i, 1, true);
-      epilogue_max(1);
-    } else {
-      epilogue_max(0);
-    }
-    finish(pv_local);  // the last tile always ends a document
-  }
+  // Tile i lives in ring slot i % kPrefetch; the last tile always ends a
+  // document.
+  for (int i = 0; i < ntiles; ++i) step(i);
   // No LDS-destination load may still be in flight when the wave ends.
   vm_wait_lds<0>();
 
