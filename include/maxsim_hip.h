@@ -54,6 +54,13 @@ int msim_get_docs_per_wave(void);
  * (cuda_extension.cu:1629-1692 returns full score rows). */
 int msim_set_fused_topk(int mode);
 int msim_get_fused_topk(void);
+/* Work split of the int8-query scan: 0 (default) = documents to waves
+ * longest first, each to the least-loaded wave (whole corpus addressed from
+ * one base; up to 2^25 tokens and 2^24 documents, beyond that as 1);
+ * 1 = contiguous document ranges balanced by cost.  Results are identical.
+ * No counterpart in the reference (its kernels take one block per document). */
+int msim_set_scan_partition(int mode);
+int msim_get_scan_partition(void);
 
 /* Symmetric int4 packing on the device: pack_int4_symmetric
  * (experimental.py:218-268) with codes in _pack_signed_int4_values' nibble

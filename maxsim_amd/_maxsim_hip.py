@@ -82,6 +82,16 @@ def get_fused_topk() -> int:
     return int(_native.load().msim_get_fused_topk())
 
 
+def set_scan_partition(mode: int) -> None:
+    """Work split of the int8-query scan: 0 = longest-first document
+    assignment (default), 1 = contiguous document ranges."""
+    check(_native.load().msim_set_scan_partition(int(mode)))
+
+
+def get_scan_partition() -> int:
+    return int(_native.load().msim_get_scan_partition())
+
+
 class CudaInt4PackedDocs:
     """Resident int4 corpus (reference: CudaInt4PackedDocs, cu:2677-3306)."""
 

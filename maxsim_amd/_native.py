@@ -30,6 +30,8 @@ SIGNATURES: dict[str, list] = {
     "msim_pack_int4": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp],
     "msim_pack_int4_async": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp, c_vp],
     "msim_get_fused_topk": [],
+    "msim_set_scan_partition": [c_int],
+    "msim_get_scan_partition": [],
     # int4 handle
     "msim_int4_create": [c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_dbl, c_vp],
     "msim_int4_destroy": [c_vp],

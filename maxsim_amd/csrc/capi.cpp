@@ -15,6 +15,7 @@ namespace msim {
 thread_local std::string g_last_error;
 int g_docs_per_wave = 0;
 int g_fused_topk = 1;  // msim_set_fused_topk
+int g_scan_partition = 0;  // msim_set_scan_partition
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -99,6 +100,15 @@ extern "C" int msim_set_fused_topk(int mode) {
 }
 
 extern "C" int msim_get_fused_topk(void) { return g_fused_topk; }
+
+extern "C" int msim_set_scan_partition(int mode) {
+  return guarded([&] {
+    if (mode < 0 || mode > 1) throw InvalidArgument("scan partition mode must be 0 or 1");
+    g_scan_partition = mode;
+  });
+}
+
+extern "C" int msim_get_scan_partition(void) { return g_scan_partition; }
 
 // -------------------------------------------------------------- int4 handle
 
@@ -221,11 +231,11 @@ void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* 
 
 // Scan tables of the handle for the requested wave count (cached).
 void build_wave_info(msim_int4_docs* h, int64_t waves) {
-  if (h->partition_waves == waves) return;
+  if (h->partition_waves == waves && h->partition_mode == g_scan_partition) return;
   std::vector<int64_t> info;
   std::vector<uint64_t> tiles;
-  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, info, tiles, h->tile_stride);
-  h->num_scan_waves = (int64_t)info.size() / kWaveInfoWords;
+  build_scan_tables(h->host_offsets.data(), h->num_docs, waves, g_scan_partition == 1, info, tiles, h->tile_stride,
+                    h->num_scan_waves);
   h->wave_info.ensure(sizeof(int64_t) * std::max<size_t>(1, info.size()), "hipMalloc scan wave table");
   if (!info.empty())
     check_hip(hipMemcpy(h->wave_info.ptr, info.data(), sizeof(int64_t) * info.size(), hipMemcpyHostToDevice),
@@ -235,6 +245,7 @@ void build_wave_info(msim_int4_docs* h, int64_t waves) {
     check_hip(hipMemcpy(h->tile_table.ptr, tiles.data(), sizeof(uint64_t) * tiles.size(), hipMemcpyHostToDevice),
               "copy scan tile table to device");
   h->partition_waves = waves;
+  h->partition_mode = g_scan_partition;
 }
 
 int64_t scan_waves(const msim_int4_docs* h) {

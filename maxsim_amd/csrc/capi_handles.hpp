@@ -86,6 +86,7 @@ struct msim_int4_docs {
   int64_t max_doc_tiles = 1;    // 16-token tiles of the longest document
   std::vector<int64_t> host_offsets;
   int64_t partition_waves = 0;    // wave count the cached scan table was built for
+  int partition_mode = 0;         // msim_set_scan_partition mode it was built with
   int64_t num_scan_waves = 0;     // rows of wave_info
   int64_t tile_stride = 0;        // tile-table entries per wave
   msim::DeviceBuffer wave_info, tile_table;

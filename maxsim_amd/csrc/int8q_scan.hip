@@ -132,11 +132,11 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
 
   const auto info = as_constant(wave_info_ptr) + gw * kWaveInfoWords;
   const int64_t d0 = info[0];
-  const int ndocs = (int)info[1];
   const int64_t T0 = info[2], T1 = info[3];
   const int ntiles = (int)info[4];
   const auto tt = as_constant(tile_table) + gw * p.tile_stride;  // no wait on `info`
-  const bool has_empty = info[6] != 0;
+  const int nempty = (int)info[6];
+  const int64_t e0 = info[7];
   constexpr bool fused = kTail;  // p.topk_k > 0 exactly when kTail
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
@@ -308,14 +308,10 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // No LDS-destination load may still be in flight when the wave ends.
   vm_wait_lds<0>();
 
-  // Empty documents score 0 (lane d owns local document d).
-  if (has_empty) {
-    const int64_t off = lane <= ndocs ? offsets[d0 + lane] : 0;
-    const int64_t next = ((int64_t)__shfl_down((int)(uint32_t)((uint64_t)off >> 32), 1) << 32) |
-                         (uint32_t)__shfl_down((int)(uint32_t)(uint64_t)off, 1);
-    if (lane < ndocs && next == off) {
-      for (int b = 0; b < p.batch; ++b) put_score(scores + (int64_t)b * p.score_stride + d0 + lane, 0.0f, fused);
-    }
+  // Empty documents score 0 (the wave's entries of the empty-document list).
+  for (int e = lane; e < nempty; e += kWave) {
+    const int64_t doc = wave_info_ptr[p.num_waves * kWaveInfoWords + e0 + e];
+    for (int b = 0; b < p.batch; ++b) put_score(scores + (int64_t)b * p.score_stride + doc, 0.0f, fused);
   }
   if constexpr (!fused) return;
 

@@ -38,20 +38,21 @@ hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int
                                const int64_t* d_offsets, float* d_out, hipStream_t stream);
 
 // Full-corpus scan over pre-quantised query rows (int8q_scan.hip).  Each wave
-// owns a contiguous range of at most kScanMaxDocsPerWave documents, described
-// by kWaveInfoWords int64 words:
-//   [0] d0          first document
-//   [1] ndocs       documents [d0, d0 + ndocs)
-//   [2] T0, [3] T1  token range of the wave (offsets[d0], offsets[d0 + ndocs]),
-//                   with (T1 - T0) * 64 < 2^31
+// scores a set of documents (scan_tables.cpp), described by kWaveInfoWords
+// int64 words:
+//   [0] d0          document base (0 when the wave's documents are scattered)
+//   [1] ndocs       non-empty documents of the wave
+//   [2] T0, [3] T1  token range the wave's tiles lie in, (T1 - T0) * 64 < 2^31
 //   [4] ntiles      16-token tiles of the wave: sum over documents of ceil(len / 16)
 //   [5] tab0        index of the wave's first entry in the tile table
-//   [6] has_empty   the wave has empty documents
+//   [6] nempty      empty documents the wave writes 0 for
+//   [7] e0          their first entry in the empty-document list, which
+//                   follows the num_waves rows in the same buffer
 // The table is padded to whole workgroups with waves of no tiles.  Tile table
 // entries (one per tile, then kScanPrefetch + 1 padding entries per wave):
 // low 32 bits the tile's first token relative to T0 (kScanPastEnd for
 // padding), then (rows - 1) in bits 32..36, "last tile of its document" in
-// bit 37 and the document's index relative to d0 in bits 40..47.
+// bit 37 and the document's index relative to d0 in bits 40..63.
 constexpr int kWaveInfoWords = 8;
 constexpr int kScanMaxDocsPerWave = 63;
 constexpr int kScanWavesPerGroup = 4;
@@ -101,8 +102,11 @@ hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t
 // result may hold more rows: ranges are split at kScanMaxDocsPerWave
 // documents and 2^25 tokens, and padded to whole workgroups).  Each wave's
 // tile entries start at wave * tile_stride.
-void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves,
-                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table, int64_t& tile_stride);
+// `contiguous` forces contiguous document ranges (otherwise used only for
+// corpora beyond 2^25 tokens or 2^24 documents).
+void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves, bool contiguous,
+                       std::vector<int64_t>& wave_info, std::vector<uint64_t>& tile_table, int64_t& tile_stride,
+                       int64_t& num_waves);
 
 // Generalized scoring (score.hip): int4 or sign-bit documents, optional int4
 // residual stream, 1 (int8) or 3 (fp32 split into int8 limbs) query limbs,

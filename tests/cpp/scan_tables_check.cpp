@@ -1,0 +1,43 @@
+// Property check of build_scan_tables (scan_tables.cpp) on random ragged corpora,
+// both partition modes: every token of every non-empty document lies in a tile
+// of its own document, exactly one tile per document is marked last and ends
+// at the document end, every empty document is listed once, tile slots are
+// padded, and the wave count is a multiple of the workgroup size.
+#include <cstdio>
+#include <vector>
+#include <cstdint>
+#include <random>
+#include "internal.hpp"
+int main() {
+  std::mt19937 rng(1);
+  for (int trial = 0; trial < 200; ++trial) {
+    int n = 1 + rng() % 300; std::vector<int64_t> off(n + 1, 0);
+    for (int d = 0; d < n; ++d) off[d + 1] = off[d] + (rng() % 5 == 0 ? 0 : rng() % 200);
+    for (int contiguous = 0; contiguous < 2; ++contiguous) {
+      int64_t waves = 1 + rng() % 64;
+      std::vector<int64_t> info; std::vector<uint64_t> table; int64_t stride, nw;
+      msim::build_scan_tables(off.data(), n, waves, contiguous, info, table, stride, nw);
+      std::vector<int> seen_tok(off[n], 0), seen_empty(n, 0), doc_tiles_last(n, 0);
+      for (int64_t w = 0; w < nw; ++w) {
+        const int64_t* r = &info[w * 8];
+        for (int64_t i = 0; i < r[4]; ++i) {
+          uint64_t e = table[r[5] + i]; int64_t start = (int64_t)(e & 0xFFFFFFFFu) + r[2];
+          uint32_t hi = (uint32_t)(e >> 32); int rows = (hi & 31) + 1; bool last = (hi >> 5) & 1; int64_t doc = (hi >> 8) + r[0];
+          if (doc < 0 || doc >= n || start < off[doc] || start + rows > off[doc + 1]) { printf("BAD tile w%ld\n", (long)w); return 1; }
+          for (int t = 0; t < rows; ++t) seen_tok[start + t]++;
+          if (last) doc_tiles_last[doc]++;
+          if (last != (start + rows == off[doc + 1])) { printf("BAD last\n"); return 1; }
+        }
+        for (int64_t i = r[4]; i < stride; ++i) if (table[r[5] + i] != msim::kScanPastEnd) { printf("BAD pad\n"); return 1; }
+        for (int64_t e = 0; e < r[6]; ++e) seen_empty[info[nw * 8 + r[7] + e]]++;
+      }
+      for (int d = 0; d < n; ++d) {
+        bool empty = off[d + 1] == off[d];
+        if (empty ? (seen_empty[d] != 1 || doc_tiles_last[d]) : (doc_tiles_last[d] != 1 || seen_empty[d])) { printf("BAD doc %d\n", d); return 1; }
+      }
+      for (int64_t t = 0; t < off[n]; ++t) if (seen_tok[t] < 1) { printf("BAD token %ld\n", (long)t); return 1; }
+      if (nw % 4) { printf("BAD nw\n"); return 1; }
+    }
+  }
+  printf("ok\n");
+}

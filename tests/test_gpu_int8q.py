@@ -109,3 +109,32 @@ def test_int8q_workspace_growth_after_larger_batch(gpu, oracle):
     for shape in [(1, 4), (8, 32), (2, 3)]:
         query = rng.standard_normal((*shape, 128)).astype(np.float32)
         np.testing.assert_array_equal(device.data.maxsim_batch_int8q(query), _scores(oracle, packed, query))
+
+
+@pytest.fixture
+def scan_partition():
+    from maxsim_amd import _maxsim_hip
+
+    yield _maxsim_hip.set_scan_partition
+    _maxsim_hip.set_scan_partition(0)
+
+
+@pytest.mark.parametrize("lengths", [(0, 40), (60, 200), (1, 3)])
+def test_int8q_scan_partitions_agree_with_oracle(gpu, oracle, scan_partition, lengths):
+    """Longest-first document assignment (default) and contiguous ranges
+    (msim_set_scan_partition(1), the large-corpus path) both equal the oracle
+    bit for bit, scores and top-k."""
+    lo, hi = lengths
+    docs, offsets = ragged_fixture(1500, seed=lo + hi, lo=lo, hi=hi, empty=7)
+    packed = pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    query = np.random.default_rng(3).standard_normal((4, 32, 128)).astype(np.float32)
+    expected = _scores(oracle, packed, query)
+    ref_s, ref_i = oracle.topk(expected, 10)
+    for mode in (0, 1):
+        print(f"case partition={mode} lengths={lengths}", flush=True)
+        scan_partition(mode)
+        device = int4_to_device(packed)
+        np.testing.assert_array_equal(device.data.maxsim_batch_int8q(query), expected)
+        top_s, top_i = device.data.topk_batch_int8q(query, 10)
+        np.testing.assert_array_equal(top_i, ref_i)
+        np.testing.assert_array_equal(top_s, ref_s)
