@@ -11,11 +11,8 @@ namespace msim {
 
 namespace {
 
-constexpr uint64_t kEntryStartMask = 0xFFFFFFFFFFull;
-
 __device__ __forceinline__ uint64_t tile_entry(int64_t start, int64_t rows, bool last, bool empty, int64_t local) {
-  return ((uint64_t)start & kEntryStartMask) | ((uint64_t)(rows - 1) << 40) | ((uint64_t)last << 45) |
-         ((uint64_t)empty << 46) | ((uint64_t)local << 48);
+  return score_tile_entry(start, rows, last, empty, local);
 }
 
 // One thread per (group, wave): the wave's candidates [t0, t0 + n) with

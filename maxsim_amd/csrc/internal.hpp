@@ -112,11 +112,19 @@ void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves, 
 // residual stream, 1 (int8) or 3 (fp32 split into int8 limbs) query limbs,
 // reducers.  Targets are documents or candidate positions, walked from a
 // host-built table (build_score_tables): per wave kScoreInfoWords int64
-// words {first target, targets, tiles, first tile-table entry}, padded to
-// whole workgroups; per tile one entry: bits 0..39 first token, 40..43
-// rows - 1, 45 last tile of its target, 46 empty target (no tokens, token
-// 0 is read and masked), 48..63 target index relative to the wave's first;
+// words {target base, targets, tiles, first tile-table entry}, padded to
+// whole workgroups; per tile one entry: bits 0..33 first token, 34..37
+// rows - 1, 38 last tile of its target, 39 empty target (no tokens, token 0
+// is read and masked), 40..63 target index relative to the wave's base;
 // one padding entry (token 0) follows every wave's tiles.
+constexpr uint64_t kTileStartMask = (uint64_t(1) << 34) - 1;
+constexpr int kTileRowsShift = 34, kTileLastShift = 38, kTileEmptyShift = 39, kTileLocalShift = 40;
+__host__ __device__ inline uint64_t score_tile_entry(int64_t start, int64_t rows, bool last, bool empty,
+                                                     int64_t local) {
+  return ((uint64_t)start & kTileStartMask) | ((uint64_t)(rows - 1) << kTileRowsShift) |
+         ((uint64_t)last << kTileLastShift) | ((uint64_t)empty << kTileEmptyShift) |
+         ((uint64_t)local << kTileLocalShift);
+}
 constexpr int kScoreInfoWords = 4;
 enum : int { kDocInt4 = 0, kDocSign = 1 };
 enum : int { kRedMax = 0, kRedTop2 = 1, kRedTop4 = 2, kRedLse = 3 };

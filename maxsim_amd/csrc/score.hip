@@ -233,8 +233,8 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
   // Every load is unconditional: rows past a short document read its last
   // token again (masked below); table padding entries point at token 0.
   auto load = [&](uint64_t e, Tile& t) {
-    const int64_t start = (int64_t)(e & 0xFFFFFFFFFFull);
-    const int rows1 = (int)((e >> 40) & 15);
+    const int64_t start = (int64_t)(e & kTileStartMask);
+    const int rows1 = (int)((e >> kTileRowsShift) & 15);
     const int64_t tok = start + min(c, rows1);
     if constexpr (DOC == kDocInt4)
       t.a.w = *reinterpret_cast<const v4u*>(p.codes + tok * 64 + 16 * g);
@@ -260,9 +260,9 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
   for (int i = 0; i < ntiles; ++i) {
     const uint64_t en = tt[i + 1];
     load(en, nxt);
-    const int local = (int)(e >> 48);
-    const bool last = ((e >> 45) & 1) != 0;
-    const int rows = ((e >> 46) & 1) ? 0 : (int)((e >> 40) & 15) + 1;
+    const int local = (int)(e >> kTileLocalShift);
+    const bool last = ((e >> kTileLastShift) & 1) != 0;
+    const int rows = ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
     if (fresh) {
       const int64_t tg = t0 + local;
       const int64_t doc = targets ? targets[tg] : tg;

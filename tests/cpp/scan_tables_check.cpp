@@ -1,8 +1,12 @@
-// Property check of build_scan_tables (scan_tables.cpp) on random ragged corpora,
-// both partition modes: every token of every non-empty document lies in a tile
-// of its own document, exactly one tile per document is marked last and ends
-// at the document end, every empty document is listed once, tile slots are
-// padded, and the wave count is a multiple of the workgroup size.
+// Property checks of the host work splits on random ragged corpora.
+// build_scan_tables (scan_tables.cpp), both partition modes: every token of
+// every non-empty document lies in a tile of its own document, exactly one
+// tile per document is marked last and ends at the document end, every empty
+// document is listed once, tile slots are padded, and the wave count is a
+// multiple of the workgroup size.  build_score_tables (score_tables.cpp),
+// documents or candidate targets (with duplicates): every target's tokens are
+// covered by its tiles in order, exactly once, its last tile flagged, an empty
+// target gets one empty tile, and every wave ends with a padding entry.
 #include <cstdio>
 #include <vector>
 #include <cstdint>
@@ -37,6 +41,48 @@ int main() {
       }
       for (int64_t t = 0; t < off[n]; ++t) if (seen_tok[t] < 1) { printf("BAD token %ld\n", (long)t); return 1; }
       if (nw % 4) { printf("BAD nw\n"); return 1; }
+    }
+  }
+  // build_score_tables
+  for (int trial = 0; trial < 200; ++trial) {
+    int n = 1 + rng() % 300; std::vector<int64_t> off(n + 1, 0);
+    for (int d = 0; d < n; ++d) off[d + 1] = off[d] + (rng() % 5 == 0 ? 0 : rng() % 200);
+    std::vector<int64_t> targets;
+    const bool cand = trial % 2 == 1;
+    const int nt = cand ? 1 + rng() % 200 : n;
+    for (int t = 0; t < nt && cand; ++t) targets.push_back(rng() % n);
+    std::vector<int64_t> info; std::vector<uint64_t> tiles;
+    msim::build_score_tables(off.data(), cand ? targets.data() : nullptr, nt, 1 + rng() % 64, info, tiles);
+    std::vector<int64_t> next_tok(nt, -1); std::vector<int> lasts(nt, 0);
+    const int64_t nw = (int64_t)info.size() / msim::kScoreInfoWords;
+    if (nw % 4) { printf("BAD score nw\n"); return 1; }
+    for (int64_t w = 0; w < nw; ++w) {
+      const int64_t* r = &info[w * msim::kScoreInfoWords];
+      for (int64_t i = 0; i < r[2]; ++i) {
+        const uint64_t e = tiles[r[3] + i];
+        const int64_t start = (int64_t)(e & msim::kTileStartMask);
+        const int rows = (int)((e >> msim::kTileRowsShift) & 15) + 1;
+        const bool last = (e >> msim::kTileLastShift) & 1, empty = (e >> msim::kTileEmptyShift) & 1;
+        const int64_t t = r[0] + (int64_t)(e >> msim::kTileLocalShift);
+        if (t < 0 || t >= nt) { printf("BAD score target\n"); return 1; }
+        const int64_t d = cand ? targets[t] : t;
+        if (empty) {
+          if (off[d + 1] != off[d] || !last) { printf("BAD score empty\n"); return 1; }
+        } else {
+          const int64_t expect = next_tok[t] < 0 ? off[d] : next_tok[t];
+          if (start != expect || start + rows > off[d + 1]) { printf("BAD score tile\n"); return 1; }
+          next_tok[t] = start + rows;
+          if (last != (start + rows == off[d + 1])) { printf("BAD score last\n"); return 1; }
+        }
+        lasts[t] += last ? 1 : 0;
+      }
+      const uint64_t pad = tiles[r[3] + r[2]];
+      if ((pad & msim::kTileStartMask) != 0 || ((pad >> msim::kTileLastShift) & 1)) { printf("BAD score pad\n"); return 1; }
+    }
+    for (int t = 0; t < nt; ++t) {
+      const int64_t d = cand ? targets[t] : t;
+      if (lasts[t] != 1) { printf("BAD score lasts %d\n", t); return 1; }
+      if (off[d + 1] != off[d] && next_tok[t] != off[d + 1]) { printf("BAD score cover\n"); return 1; }
     }
   }
   printf("ok\n");
