@@ -27,7 +27,9 @@
 //  * per tile: 16 MFMAs, then the VALU epilogue (scale, running max); the
 //    two waves of a SIMD overlap one's MFMAs with the other's VALU work;
 //  * at a document end: cross-lane max over the four lane groups and numpy's
-//    float64 pairwise sum over query tokens;
+//    float64 pairwise sum over query tokens; for 32-token queries entirely
+//    in registers (permlane swaps scatter batch row b to lane group b, DPP
+//    moves order the pairwise sum), otherwise through LDS;
 //  * fused selection (ScanArgs::topk_k > 0): scores are stored write-through
 //    and every workgroup takes a ticket once its stores have completed; the
 //    last one selects each batch row's top-k (topk_block.hpp, tail form),
@@ -49,6 +51,33 @@ static_assert(kScanTailMaxK <= kWave, "fused selection k");
 __device__ __forceinline__ float max_over_groups(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// Reduce-scatter of eight per-lane tile maxima over the four lane groups:
+// group g ends with the maxima of tiles 2g (t0) and 2g + 1 (t1).  A
+// permlane32 swap of (m[a], m[a + 4]) leaves tile a in lanes 0..31 and tile
+// a + 4 in lanes 32..63, each reduced over the two halves; a permlane16 swap
+// of (x[a], x[a + 2]) then reduces over the two rows of each half.  Tiles
+// past NT are -inf.
+template <int NT>
+__device__ __forceinline__ void max_scatter_groups(const float (&m)[NT], float& t0, float& t1) {
+  auto mm = [&](int j) { return j < NT ? m[j] : kNegInf; };
+  auto swap_max = [](float a, float b, auto swap) {
+    const auto r = swap(__float_as_uint(a), __float_as_uint(b));
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  };
+  auto sw32 = [](uint32_t a, uint32_t b) { return __builtin_amdgcn_permlane32_swap(a, b, false, false); };
+  auto sw16 = [](uint32_t a, uint32_t b) { return __builtin_amdgcn_permlane16_swap(a, b, false, false); };
+  float x[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) x[a] = swap_max(mm(a), mm(a + 4), sw32);
+  t0 = swap_max(x[0], x[2], sw16);
+  t1 = swap_max(x[1], x[3], sw16);
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
 }
 
 // A score store; write-through (agent-scope atomic) when the launch selects
@@ -219,9 +248,39 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       m[j] = max3_op(max3_op(m[j], x0, x1), x2, x3);
     }
   };
+  // 32-token queries: batch row g is summed by lane group g in registers
+  // (tokens c and 16 + c in lane c); its query scales are read once here.
+  const bool q32 = NT % 2 == 0 && p.query_tokens == 32;
+  float sig0 = 0.0f, sig1 = 0.0f;
+  if (q32) {
+    sig0 = qs[32 * g + c];
+    sig1 = qs[32 * g + 16 + c];
+  }
+
   // Document end: per-row maxima over the four lane groups, then the score of
   // local document `local`.
   auto finish = [&](int local) {
+    if (q32) {
+      // numpy's pairwise float64 sum of 32 terms: accumulator k < 8 adds
+      // tokens k, k + 8, k + 16, k + 24 in that order (lane k; row_ror:8
+      // brings lane k + 8's products), then ((r0 + r1) + (r2 + r3)) +
+      // ((r4 + r5) + (r6 + r7)) by lane swaps within quads (every lane of
+      // quad 0 then holds the first half, every lane of quad 1 the second)
+      // and a half-row mirror (lane 0 reads lane 7).
+      float t0, t1;
+      max_scatter_groups<NT>(m, t0, t1);
+      const double p0 = (double)t0 * (double)sig0, p1 = (double)t1 * (double)sig1;
+      double r = __dadd_rn(p0, dpp_f64<0x128>(p0));
+      r = __dadd_rn(r, p1);
+      r = __dadd_rn(r, dpp_f64<0x128>(p1));
+      r = __dadd_rn(r, dpp_f64<0xB1>(r));   // quad_perm [1,0,3,2]
+      r = __dadd_rn(r, dpp_f64<0x4E>(r));   // quad_perm [2,3,0,1]
+      r = __dadd_rn(r, dpp_f64<0x141>(r));  // row_half_mirror
+      if (c == 0 && g < p.batch) put_score(scores + d0 + local + (int64_t)g * p.score_stride, (float)(r * p.scale), fused);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) m[j] = kNegInf;
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NT; ++j) m[j] = max_over_groups(m[j]);
     if (g == 0) {
@@ -241,11 +300,12 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   int slot = 0;
 
   // One step for tile i (in `w`, ring slot `slot`): refill of that slot,
-  // read-back of the next tile, the tile's MFMAs and its epilogue.  (A
-  // double-buffered accumulator set, MFMAs of tile i interleaved with the
-  // epilogue of tile i - 1, measured slower: the other wave of the SIMD
-  // already overlaps one wave's MFMAs with another's VALU work, and the
-  // second set costs 64 VGPRs.)
+  // read-back of the next tile, the tile's MFMAs and its epilogue.  The loop
+  // is bound by instruction issue (an MFMA takes a VALU issue slot).
+  // Measured no faster: MFMAs of tile i interleaved with the epilogue of
+  // tile i - 1 (one or two accumulator sets), accumulators in AGPRs, and a
+  // zero C operand for full tiles (saves the register copies, but the
+  // compiler then interleaves dependent MFMAs with the epilogue).
   auto step = [&](int i) {
     v4i lo, hi;
 #pragma unroll

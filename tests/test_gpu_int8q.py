@@ -22,7 +22,7 @@ def _scores(oracle, packed, query):
 
 
 @pytest.mark.parametrize("granularity", ["token", "tensor"])
-@pytest.mark.parametrize("shape", [(2, 5), (1, 1), (3, 8), (4, 32), (5, 24), (9, 16), (2, 130)])
+@pytest.mark.parametrize("shape", [(2, 5), (1, 1), (3, 8), (4, 32), (1, 32), (3, 32), (5, 24), (9, 16), (2, 130)])
 def test_int8q_scores_bit_exact_ragged(gpu, oracle, granularity, shape):
     b, q = shape
     print(f"case granularity={granularity} B={b} Q={q}", flush=True)
