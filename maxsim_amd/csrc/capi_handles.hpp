@@ -12,6 +12,7 @@ namespace msim {
 // monotonically, freed with the handle; cu:3057-3067).
 struct ScoreWorkspace {
   DeviceBuffer qpack, colmul, qsum, weights, pooled, query, qbits;
+  DeviceBuffer qpack_alt;  // the query also in the int4 layout (QueryInput::alt_int4)
   DeviceBuffer full_info, full_tiles;  // cached whole-corpus tables
   int64_t full_key = -1;               // wave count the cached tables were built for
   int64_t full_waves = 0;              // waves in the cached table
@@ -19,7 +20,7 @@ struct ScoreWorkspace {
   // cascade: coarse scores, top-M candidates (scores / ids), fine scores
   DeviceBuffer coarse, top_m_scores, top_m_ids, fine;
   uint64_t bytes() const {
-    return qpack.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + query.cap + qbits.cap + full_info.cap +
+    return qpack.cap + qpack_alt.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + query.cap + qbits.cap + full_info.cap +
            full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap + coarse.cap + top_m_scores.cap +
            top_m_ids.cap + fine.cap;
   }
@@ -32,6 +33,8 @@ struct QueryInput {
   int limbs = 3;                     // 3: fp32 split into int8 limbs, 1: int8
   bool recip = false;                // int8 rounding q * (1 / sigma) (binary int8q)
   bool quantized = false;            // the workspace already holds this query in this layout
+  bool alt_int4 = false;             // also quantise into qpack_alt in the int4 layout
+  bool from_alt = false;             // score the rows an earlier alt_int4 call left in qpack_alt
 };
 
 // The document streams and scales of one scoring call.
@@ -60,7 +63,17 @@ struct Targets {
   const int64_t* device = nullptr;
   const int64_t* d_offsets = nullptr;
   int64_t max_doc_tiles = 1;
+  bool tables_ready = false;  // the candidate tables are already in the workspace (select_topm wrote them)
 };
+
+// Wave layout of a per-row candidate rescoring pass (device targets): what
+// run_generic_score uses, so that the candidate selector can write the
+// tables for it.
+struct CandidateLayout {
+  int64_t waves = 0, per_wave = 0, cap = 0;
+};
+CandidateLayout candidate_layout(int64_t batch, int64_t query_tokens, int limbs, int64_t per_target,
+                                 int64_t max_doc_tiles);
 
 // Scores of `batch` x `query_tokens` query rows against the targets into
 // d_out[b * out_stride + t] (and d_iout[b * targets + t] as int32 if set).

@@ -26,6 +26,19 @@ T* upload_vec(DeviceBuffer& buf, const std::vector<T>& v, const char* what) {
 
 }  // namespace
 
+CandidateLayout candidate_layout(int64_t batch, int64_t query_tokens, int limbs, int64_t per_target,
+                                 int64_t max_doc_tiles) {
+  const int64_t rpp = score_rows_per_pass(limbs, query_tokens);
+  const int64_t subs = ceil_div(query_tokens, rpp);
+  int64_t waves = ceil_div((int64_t)device_cu_count() * 8, batch * subs);
+  waves = std::max<int64_t>(1, std::min(waves, per_target));
+  CandidateLayout cl;
+  cl.per_wave = ceil_div(per_target, waves);
+  cl.waves = ceil_div(ceil_div(per_target, cl.per_wave), 4) * 4;
+  cl.cap = cl.per_wave * std::max<int64_t>(1, max_doc_tiles) + 1;
+  return cl;
+}
+
 void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int64_t num_tokens,
                        const DocStreams& s, const QueryInput& q, int reducer, float temperature,
                        int64_t batch, int64_t query_tokens, const float* h_row_weights, const Targets& t,
@@ -49,7 +62,8 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   ws.qpack.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs");
   ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
   ws.qsum.ensure(sizeof(int32_t) * limbs * rows_padded, "hipMalloc query limb sums");
-  if (q.quantized) {
+  if (q.alt_int4) ws.qpack_alt.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs (int4 layout)");
+  if (q.quantized || q.from_alt) {
     // reuse the workspace's quantised rows
   } else if (q.d_qbits)
     check_hip(launch_quantize_bits(q.d_qbits, rows, rows_padded, ws.qpack.as<int8_t>(), ws.colmul.as<float>(),
@@ -59,7 +73,8 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
     // A sign stream paired with an int4 residual is unpacked in the int4
     // lane order, so both share the int4 query layout.
     check_hip(launch_quantize_limbs(q.d_query, rows, rows_padded, limbs, s.residual ? kDocInt4 : s.doc, q.recip,
-                                    ws.qpack.as<int8_t>(), ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream),
+                                    ws.qpack.as<int8_t>(), ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream,
+                                    kDocInt4, q.alt_int4 ? ws.qpack_alt.as<int8_t>() : nullptr),
               "launch query quantize kernel");
 
   // 2. Reducer weights, one per query row (padding rows 0).
@@ -83,15 +98,16 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   const int64_t* d_targets = nullptr;
   if (t.device) {
     // Candidate lists on the device: fixed-size target ranges per wave,
-    // tables written by candidate_tables_kernel.
-    const int64_t per_wave = ceil_div(per_target, waves);
-    const int64_t w4 = ceil_div(ceil_div(per_target, per_wave), 4) * 4;
-    const int64_t cap = per_wave * std::max<int64_t>(1, t.max_doc_tiles) + 1;
+    // tables written by candidate_tables_kernel (or already by the selector).
+    if (!t.per_row) throw InvalidArgument("device candidate lists must be per batch row");
+    const CandidateLayout cl = candidate_layout(batch, query_tokens, limbs, per_target, t.max_doc_tiles);
+    const int64_t w4 = cl.waves;
     ws.cand_info.ensure(sizeof(int64_t) * groups * w4 * kScoreInfoWords, "hipMalloc candidate wave table");
-    ws.cand_tiles.ensure(sizeof(uint64_t) * groups * w4 * cap, "hipMalloc candidate tile table");
-    check_hip(launch_candidate_tables(t.device, per_target, groups, t.d_offsets, w4, per_wave, cap,
-                                      ws.cand_info.as<int64_t>(), ws.cand_tiles.as<uint64_t>(), stream),
-              "launch candidate table kernel");
+    ws.cand_tiles.ensure(sizeof(uint64_t) * groups * w4 * cl.cap, "hipMalloc candidate tile table");
+    if (!t.tables_ready)
+      check_hip(launch_candidate_tables(t.device, per_target, groups, t.d_offsets, w4, cl.per_wave, cl.cap,
+                                        ws.cand_info.as<int64_t>(), ws.cand_tiles.as<uint64_t>(), stream),
+                "launch candidate table kernel");
     a.wave_info = ws.cand_info.as<int64_t>();
     a.tiles = ws.cand_tiles.as<uint64_t>();
     a.num_waves = w4;
@@ -150,7 +166,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   a.rmul = s.rmul;
   a.targets = d_targets;
   a.targets_grp_stride = t.per_row ? t.count : 0;
-  a.qpack = ws.qpack.as<int8_t>();
+  a.qpack = q.from_alt ? ws.qpack_alt.as<int8_t>() : ws.qpack.as<int8_t>();
   a.rows_padded = rows_padded;
   a.colmul = ws.colmul.as<float>();
   a.qsum = ws.qsum.as<int32_t>();
@@ -697,18 +713,32 @@ void check_cascade(int64_t k, int64_t m, int64_t num_docs) {
 // Coarse scores of every document -> the top-M candidates of each batch row
 // (score desc, document asc), put in document order -> fine scores of the
 // candidates -> top-k, ties by document id (cascade.py:294-453), all on the
-// device.  coarse(d_scores) and fine(d_candidate_ids, d_scores) enqueue the
-// two scoring passes.
+// device.  coarse(d_scores) and fine(d_candidate_ids, d_scores,
+// tables_ready) enqueue the two scoring passes; `layout` (the rescoring
+// pass's candidate_layout) lets the selector write the rescoring tables
+// itself, one launch fewer (tables_ready is then true).
 template <typename Coarse, typename Fine>
 void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t k, int64_t m, Coarse coarse,
-                    Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
+                    Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream, const CandidateLayout& layout,
+                    const int64_t* d_offsets) {
   ws.coarse.ensure(sizeof(float) * batch * num_docs, "hipMalloc cascade coarse scores");
   coarse(ws.coarse.as<float>());
   ws.top_m_ids.ensure(sizeof(int64_t) * batch * m, "hipMalloc cascade candidates");
+  bool tables_ready = false;
   if (num_docs <= kSortMaxRow) {
+    ws.cand_info.ensure(sizeof(int64_t) * batch * layout.waves * kScoreInfoWords, "hipMalloc candidate wave table");
+    ws.cand_tiles.ensure(sizeof(uint64_t) * batch * layout.waves * layout.cap, "hipMalloc candidate tile table");
+    CandidateTables tab;
+    tab.d_offsets = d_offsets;
+    tab.waves = layout.waves;
+    tab.per_wave = layout.per_wave;
+    tab.cap = layout.cap;
+    tab.d_info = ws.cand_info.as<int64_t>();
+    tab.d_tiles = ws.cand_tiles.as<uint64_t>();
     check_hip(launch_select_topm(ws.coarse.as<float>(), batch, num_docs, num_docs, m, ws.top_m_ids.as<int64_t>(),
-                                 stream),
+                                 stream, &tab),
               "launch cascade candidate selection");
+    tables_ready = true;
   } else {
     ws.top_m_scores.ensure(sizeof(float) * batch * m, "hipMalloc cascade candidate scores");
     check_hip(launch_topk(ws.coarse.as<float>(), batch, num_docs, num_docs, m, nullptr, ws.top_m_scores.as<float>(),
@@ -717,7 +747,7 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
     check_hip(launch_sort_rows(ws.top_m_ids.as<int64_t>(), batch, m, stream), "launch candidate sort");
   }
   ws.fine.ensure(sizeof(float) * batch * m, "hipMalloc cascade fine scores");
-  fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>());
+  fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>(), tables_ready);
   check_hip(launch_topk(ws.fine.as<float>(), batch, m, m, k, ws.top_m_ids.as<int64_t>(), d_top_s, d_top_i, stream),
             "launch cascade final selection");
 }
@@ -769,19 +799,21 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, qi, red, (float)temperature, batch,
                               query_tokens, wp, Targets{}, d, h->num_docs, nullptr, nullptr);
           },
-          [&](const int64_t* ids, float* d) {
+          [&](const int64_t* ids, float* d, bool tables_ready) {
             Targets t;
             t.device = ids;
             t.count = candidates;
             t.per_row = true;
             t.d_offsets = h->offsets.as<int64_t>();
             t.max_doc_tiles = h->max_doc_tiles;
+            t.tables_ready = tables_ready;
             QueryInput again = qi;
             again.quantized = true;
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, again, red, (float)temperature, batch,
                               query_tokens, wp, t, d, candidates, nullptr, nullptr);
           },
-          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr);
+          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr,
+          candidate_layout(batch, query_tokens, qi.limbs, candidates, h->max_doc_tiles), h->offsets.as<int64_t>());
     }
     copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
   });
@@ -826,24 +858,32 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
               "launch topk selection kernel");
     return;
   }
+  // One quantisation for both passes: the prefix pass's sign layout, and the
+  // int4 layout the fused pass reads (its sign stream is unpacked in the int4
+  // lane order).
+  QueryInput coarse_q = qi;
+  coarse_q.alt_int4 = true;
+  QueryInput fine_q = qi;
+  fine_q.from_alt = true;
   cascade_device(
       h->ws, batch, h->num_docs, k, m,
       [&](float* d) {
-        run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, qi, kRedMax, 1.0f, batch, query_tokens,
+        run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, coarse_q, kRedMax, 1.0f, batch, query_tokens,
                           nullptr, Targets{}, d, h->num_docs, nullptr, stream);
       },
-      [&](const int64_t* ids, float* d) {
-        // The fused pass reads its query in the int4 layout: quantised again.
+      [&](const int64_t* ids, float* d, bool tables_ready) {
         Targets t;
         t.device = ids;
         t.count = m;
         t.per_row = true;
         t.d_offsets = h->offsets.as<int64_t>();
         t.max_doc_tiles = h->max_doc_tiles;
-        run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, kRedMax, 1.0f, batch, query_tokens,
+        t.tables_ready = tables_ready;
+        run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, fine_q, kRedMax, 1.0f, batch, query_tokens,
                           nullptr, t, d, m, nullptr, stream);
       },
-      d_top_s, d_top_i, stream);
+      d_top_s, d_top_i, stream, candidate_layout(batch, query_tokens, qi.limbs, m, h->max_doc_tiles),
+      h->offsets.as<int64_t>());
 }
 
 }  // namespace

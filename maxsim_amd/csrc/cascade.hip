@@ -15,24 +15,22 @@ __device__ __forceinline__ uint64_t tile_entry(int64_t start, int64_t rows, bool
   return score_tile_entry(start, rows, last, empty, local);
 }
 
-// One thread per (group, wave): the wave's candidates [t0, t0 + n) with
-// n <= per_wave, and their tiles at tiles[(g * waves + w) * cap ...]; the
-// host sizes cap as per_wave * (largest document's tile count) + 1.
-__global__ __launch_bounds__(256) void candidate_tables_kernel(const int64_t* __restrict__ cands, int64_t m,
-                                                               int64_t groups, const int64_t* __restrict__ offsets,
-                                                               int64_t waves, int64_t per_wave, int64_t cap,
-                                                               int64_t* __restrict__ info,
-                                                               uint64_t* __restrict__ tiles) {
-  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (id >= groups * waves) return;
-  const int64_t g = id / waves, w = id % waves;
+// Tables of wave w of group g: its candidates [t0, t0 + n) of the group's m
+// (n <= per_wave; cand(i) gives the group's i-th document), their tiles at
+// tiles[(g * waves + w) * cap ...]; the host sizes cap as per_wave *
+// (largest document's tile count) + 1.
+template <typename Cand>
+__device__ void candidate_wave_tables(Cand cand, int64_t m, int64_t g, const int64_t* __restrict__ offsets,
+                                      int64_t waves, int64_t w, int64_t per_wave, int64_t cap,
+                                      int64_t* __restrict__ info, uint64_t* __restrict__ tiles) {
+  const int64_t id = g * waves + w;
   const int64_t t0 = min(w * per_wave, m);
   const int64_t n = min(per_wave, m - t0);
   const int64_t tab0 = id * cap;
   uint64_t* out = tiles + tab0;
   int64_t k = 0;
   for (int64_t i = 0; i < n; ++i) {
-    const int64_t doc = cands[g * m + t0 + i];
+    const int64_t doc = cand(t0 + i);
     const int64_t s = offsets[doc], e = offsets[doc + 1];
     if (s == e) {
       out[k++] = tile_entry(0, 1, true, true, i);
@@ -46,6 +44,19 @@ __global__ __launch_bounds__(256) void candidate_tables_kernel(const int64_t* __
   row[1] = n;
   row[2] = k;
   row[3] = tab0;
+}
+
+// One thread per (group, wave).
+__global__ __launch_bounds__(256) void candidate_tables_kernel(const int64_t* __restrict__ cands, int64_t m,
+                                                               int64_t groups, const int64_t* __restrict__ offsets,
+                                                               int64_t waves, int64_t per_wave, int64_t cap,
+                                                               int64_t* __restrict__ info,
+                                                               uint64_t* __restrict__ tiles) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= groups * waves) return;
+  const int64_t g = id / waves;
+  candidate_wave_tables([&](int64_t i) { return cands[g * m + i]; }, m, g, offsets, waves, id % waves, per_wave, cap,
+                        info, tiles);
 }
 
 // Ascending bitonic sort of s[0, pow2) in LDS by the whole block.
@@ -108,11 +119,14 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s
 // score key, 8 bits per round, then a stable compaction: keys above it, and
 // the first `need` keys equal to it in position order.
 __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restrict__ scores, int64_t n,
-                                                           int64_t stride, int64_t m, int64_t* __restrict__ out) {
+                                                           int64_t stride, int64_t m, int64_t* __restrict__ out,
+                                                           CandidateTables tab) {
   constexpr int E = kSortMaxRow / 1024;  // positions 4 t .. 4 t + 3 of thread t
   __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_sel[kSortMaxRow];  // the selected positions, for the tables
   __shared__ uint32_t s_wave[16];
   __shared__ uint32_t s_digit, s_above;
+  __shared__ uint32_t s_or[16], s_and[16];
   const int tid = threadIdx.x, lane = tid % kWave;
   const float* row = scores + (int64_t)blockIdx.x * stride;
   const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
@@ -124,13 +138,43 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
     valid[e] = i < n;
     key[e] = score_key(__uint_as_float(load_b32(rsrc, i * 4)));
   }
-  uint32_t prefix = 0, mask = 0, need = (uint32_t)m;
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  // The bits every key of the row shares are fixed first: scores of one
+  // query lie in a narrow range, so their top bits agree, and a radix digit
+  // over them would send every key to one histogram bin (serialised LDS
+  // atomics).  The rounds then take 8 bits at a time from the highest bit
+  // that varies.
+  uint32_t kor = 0u, kand = ~0u;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (valid[e]) {
+      kor |= key[e];
+      kand &= key[e];
+    }
+  kor = wave_reduce(kor, [](uint32_t a, uint32_t b) { return a | b; });
+  kand = wave_reduce(kand, [](uint32_t a, uint32_t b) { return a & b; });
+  if (lane == 0) {
+    s_or[tid / kWave] = kor;
+    s_and[tid / kWave] = kand;
+  }
+  __syncthreads();
+  kor = 0u;
+  kand = ~0u;
+  for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+    kor |= s_or[w];
+    kand &= s_and[w];
+  }
+  const uint32_t diff = kor ^ kand;
+  const int top = diff == 0u ? -1 : 31 - __clz(diff);  // highest varying bit
+  uint32_t mask = top >= 31 ? 0u : ~0u << (top + 1);
+  uint32_t prefix = kand & mask, need = (uint32_t)m;
+  for (int hi = top; hi >= 0; hi -= 8) {
+    const int shift = hi >= 7 ? hi - 7 : 0;
+    const uint32_t dmask = (hi - shift == 31 ? ~0u : (2u << (hi - shift)) - 1u);  // digit of bits shift..hi
     for (int i = tid; i < 256; i += blockDim.x) s_hist[i] = 0;
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&s_hist[(key[e] >> shift) & 255u], 1u);
+      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&s_hist[(key[e] >> shift) & dmask], 1u);
     __syncthreads();
     if (tid < kWave) {
       // Lane l holds digits 4l .. 4l + 3; suffix sums over the lanes from
@@ -159,7 +203,7 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
     }
     __syncthreads();
     prefix |= s_digit << shift;
-    mask |= 0xFFu << shift;
+    mask |= dmask << shift;
     need -= s_above;
     __syncthreads();
   }
@@ -181,8 +225,19 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
   uint32_t rank = block_exclusive_scan(sel, s_wave, total);
 #pragma unroll
   for (int e = 0; e < E; ++e)
-    if (take[e]) out[(int64_t)blockIdx.x * m + rank++] = E * tid + e;
+    if (take[e]) {
+      out[(int64_t)blockIdx.x * m + rank] = E * tid + e;
+      s_sel[rank] = (uint32_t)(E * tid + e);
+      ++rank;
+    }
   (void)lane;
+  if (tab.d_info == nullptr) return;
+  // The rescoring pass's tables of this row (group), from the positions in
+  // LDS: one thread per wave of the pass.
+  __syncthreads();
+  for (int64_t w = tid; w < tab.waves; w += blockDim.x)
+    candidate_wave_tables([&](int64_t i) { return (int64_t)s_sel[i]; }, m, (int64_t)blockIdx.x, tab.d_offsets,
+                          tab.waves, w, tab.per_wave, tab.cap, tab.d_info, tab.d_tiles);
 }
 
 }  // namespace
@@ -198,10 +253,14 @@ hipError_t launch_candidate_tables(const int64_t* d_cands, int64_t m, int64_t gr
 }
 
 hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, int64_t stride, int64_t m,
-                              int64_t* d_out, hipStream_t stream) {
+                              int64_t* d_out, hipStream_t stream, const CandidateTables* tables) {
   if (batch <= 0 || m <= 0) return hipSuccess;
   if (n > kSortMaxRow || m > n) return hipErrorInvalidValue;
-  select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, d_out);
+  const CandidateTables tab = tables ? *tables : CandidateTables{};
+  if (tab.d_info && (tab.d_tiles == nullptr || tab.d_offsets == nullptr || tab.waves <= 0 || tab.per_wave <= 0 ||
+                     tab.waves * tab.per_wave < m))
+    return hipErrorInvalidValue;
+  select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, d_out, tab);
   return hipGetLastError();
 }
 

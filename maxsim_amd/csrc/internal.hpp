@@ -168,7 +168,8 @@ int score_rows_per_pass(int limbs, int64_t rows);
 hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
                         hipStream_t stream);
 hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
-                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream);
+                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream,
+                                 int layout2 = 0, int8_t* qpack2 = nullptr);
 hipError_t launch_quantize_bits(const uint8_t* d_qbits, int64_t rows, int64_t rows_padded, int8_t* qpack,
                                 float* colmul, int32_t* qsum, hipStream_t stream);
 hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tokens, int64_t targets, int64_t bs,
@@ -189,8 +190,16 @@ hipError_t launch_candidate_tables(const int64_t* d_cands, int64_t m, int64_t gr
 hipError_t launch_sort_rows(int64_t* d_rows, int64_t batch, int64_t n, hipStream_t stream);
 // The m best of each row of n <= kSortMaxRow scores by (score desc,
 // position asc), output as positions in ascending order [batch, m].
+// With `tables` set, each row's block also writes the rescoring pass's
+// candidate tables (the layout launch_candidate_tables writes, group = row).
+struct CandidateTables {
+  const int64_t* d_offsets = nullptr;
+  int64_t waves = 0, per_wave = 0, cap = 0;
+  int64_t* d_info = nullptr;
+  uint64_t* d_tiles = nullptr;
+};
 hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, int64_t stride, int64_t m,
-                              int64_t* d_out, hipStream_t stream);
+                              int64_t* d_out, hipStream_t stream, const CandidateTables* tables = nullptr);
 
 // Block top-k (topk.hip): per row b of scores[b * row_stride + i], i < n, the k
 // largest by (score desc, position asc).  id_map (nullable, [batch, n]) maps a

@@ -426,21 +426,29 @@ __device__ __forceinline__ int query_byte(int d, int layout) {
 // -127, 127), r_{l+1} = r_l - a_l s_l (one rounding), s_{l+1} = s_l / 254.
 // With `recip` (one limb) the quotient is q * (1 / sigma), the binary int8
 // query rounding of cu:1328-1366.  colmul = sigma; qsum[l] = sum of limb l.
+// With qpack2, the same codes also in layout2 (a cascade's two passes).
 __global__ __launch_bounds__(256) void quantize_limbs_kernel(const float* __restrict__ query, int64_t rows,
                                                              int64_t rows_padded, int limbs, int layout,
                                                              int recip, int8_t* __restrict__ qpack,
                                                              float* __restrict__ colmul,
-                                                             int32_t* __restrict__ qsum) {
+                                                             int32_t* __restrict__ qsum, int layout2,
+                                                             int8_t* __restrict__ qpack2) {
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= rows_padded) return;
   const int d0 = 2 * lane, d1 = 2 * lane + 1;
   const int p0 = query_byte(d0, layout), p1 = query_byte(d1, layout);
+  const int p20 = query_byte(d0, layout2), p21 = query_byte(d1, layout2);
   if (row >= rows) {
     for (int l = 0; l < limbs; ++l) {
       int8_t* dst = qpack + (l * rows_padded + row) * 128;
       dst[p0] = 0;
       dst[p1] = 0;
+      if (qpack2) {
+        int8_t* dst2 = qpack2 + (l * rows_padded + row) * 128;
+        dst2[p20] = 0;
+        dst2[p21] = 0;
+      }
       if (lane == 0) qsum[l * rows_padded + row] = 0;
     }
     if (lane == 0) colmul[row] = 0.0f;
@@ -465,6 +473,11 @@ __global__ __launch_bounds__(256) void quantize_limbs_kernel(const float* __rest
     int8_t* dst = qpack + (l * rows_padded + row) * 128;
     dst[p0] = (int8_t)a;
     dst[p1] = (int8_t)b;
+    if (qpack2) {
+      int8_t* dst2 = qpack2 + (l * rows_padded + row) * 128;
+      dst2[p20] = (int8_t)a;
+      dst2[p21] = (int8_t)b;
+    }
     const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
     if (lane == 0) qsum[l * rows_padded + row] = sum;
     rx = fmaf(-(float)a, s, rx);
@@ -564,11 +577,13 @@ hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, i
 }
 
 hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
-                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream) {
+                                 bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream,
+                                 int layout2, int8_t* qpack2) {
   if (rows_padded <= 0) return hipSuccess;
   const int64_t blocks = (rows_padded + 3) / 4;
   quantize_limbs_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(d_query, rows, rows_padded, limbs, layout,
-                                                                        recip ? 1 : 0, qpack, colmul, qsum);
+                                                                        recip ? 1 : 0, qpack, colmul, qsum,
+                                                                        qpack2 ? layout2 : layout, qpack2);
   return hipGetLastError();
 }
 
