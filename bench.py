@@ -692,7 +692,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this build "
-              "scores on a single MI355X (the sharding design is written up in DESIGN.md)",
+              "scores on a single MI355X (documents would shard across GPUs with a top-k merge, not built here)",
               file=sys.stderr)
         sys.exit(2)
     if args.pack:

@@ -7,8 +7,10 @@
  * Build: make -C oracle   (plain gcc, -ffp-contract=off so every float
  * operation below is the single rounding it reads as).
  *
- * Parity pins (which check fixes each function) are listed in DESIGN.md and
- * exercised by tests/test_oracle_*.py.
+ * Every function is pinned by tests/test_oracle.py against the reference's
+ * known answers, closed forms or brute force (none is "parity unpinned");
+ * the binary LUT score also against the reference's own cpu_extension.cpp,
+ * compiled into oracle/_ref by oracle/Makefile.
  */
 #include "maxsim_oracle.h"
 
