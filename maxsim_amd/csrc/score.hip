@@ -39,6 +39,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / kWave;
 constexpr float kLimbStep = 1.0f / 254.0f;
+constexpr float kLimbStep2 = 1.0f / 64516.0f;  // 254^-2
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLowest = -3.402823466e+38f;
 
@@ -331,19 +332,31 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
       for (int rr = 0; rr < 4; ++rr) {
         // Limb dots combined smallest first; sign documents recover the
         // +-1 dot as 2 (q . bits) - sum(q).
-        float y[L];
+        // int4 documents with three limbs: the two small limbs first as one
+        // exact integer, 254 a1 + a2 (|a| <= 16 * 7 * 127 * 128 < 2^21).
+        auto limbs3 = [&](const v4i (&a)[L][NT]) {
+          const int z12 = a[1 % L][j][rr] * 254 + a[2 % L][j][rr];
+          return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
+        };
+        float Y;
+        if constexpr (L == 3 && DOC == kDocInt4) {
+          Y = limbs3(acc);
+        } else {
+          float y[L];
 #pragma unroll
-        for (int l = 0; l < L; ++l)
-          y[l] = DOC == kDocSign ? (float)(2 * acc[l][j][rr] - qsum[l][j]) : (float)acc[l][j][rr];
-        float Y = y[0];
-        if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
+          for (int l = 0; l < L; ++l)
+            y[l] = DOC == kDocSign ? (float)(2 * acc[l][j][rr] - qsum[l][j]) : (float)acc[l][j][rr];
+          Y = y[0];
+          if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
+        }
         z[rr] = Y * srow[rr];
         if constexpr (RES) {
-          float yr[L];
-#pragma unroll
-          for (int l = 0; l < L; ++l) yr[l] = (float)accr[l][j][rr];
-          float YR = yr[0];
-          if constexpr (L == 3) YR = fmaf(fmaf(yr[2], kLimbStep, yr[1]), kLimbStep, yr[0]);
+          float YR;
+          if constexpr (L == 3) {
+            YR = limbs3(accr);
+          } else {
+            YR = (float)accr[0][j][rr];
+          }
           z[rr] = z[rr] + YR * srrow[rr];
         }
       }
