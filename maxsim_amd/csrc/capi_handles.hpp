@@ -13,6 +13,7 @@ namespace msim {
 struct ScoreWorkspace {
   DeviceBuffer qpack, colmul, qsum, weights, pooled, query, qbits;
   DeviceBuffer qpack_alt;  // the query also in the int4 layout (QueryInput::alt_int4)
+  std::vector<float> weights_host;  // what `weights` holds (a repeated weight vector is not copied again)
   DeviceBuffer full_info, full_tiles;  // cached whole-corpus tables
   int64_t full_key = -1;               // wave count the cached tables were built for
   int64_t full_waves = 0;              // waves in the cached table

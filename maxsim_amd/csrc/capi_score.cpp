@@ -82,7 +82,13 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   if (h_row_weights) {
     std::vector<float> w((size_t)rows_padded, 0.0f);
     std::memcpy(w.data(), h_row_weights, sizeof(float) * rows);
-    d_weights = upload_vec(ws.weights, w, "copy reducer query weights to device");
+    if (ws.weights.ptr != nullptr && w.size() == ws.weights_host.size() &&
+        std::memcmp(w.data(), ws.weights_host.data(), sizeof(float) * w.size()) == 0) {
+      d_weights = ws.weights.as<float>();
+    } else {
+      d_weights = upload_vec(ws.weights, w, "copy reducer query weights to device");
+      ws.weights_host = std::move(w);
+    }
   }
 
   // 3. Work split.
