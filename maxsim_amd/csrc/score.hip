@@ -66,13 +66,16 @@ struct TopState {
 #pragma unroll
     for (int i = 0; i < K; ++i) t[i] = kNegInf;
   }
+  // With t sorted descending, the new i-th largest of t and v is the median
+  // of t[i - 1], t[i] and v (the maximum for i = 0): one v_med3_f32 each,
+  // all from the old values.  Only selections, so the result is exact.
   __device__ void insert(float v) {
+    float n[K];
+    n[0] = fmaxf(t[0], v);
 #pragma unroll
-    for (int i = 0; i < K; ++i) {
-      const float hi = fmaxf(t[i], v);
-      v = fminf(t[i], v);
-      t[i] = hi;
-    }
+    for (int i = 1; i < K; ++i) n[i] = __builtin_amdgcn_fmed3f(t[i - 1], t[i], v);
+#pragma unroll
+    for (int i = 0; i < K; ++i) t[i] = n[i];
   }
   __device__ void add4(const float (&z)[4], float) {
 #pragma unroll
