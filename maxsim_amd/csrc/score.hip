@@ -106,6 +106,10 @@ struct ReducerState<kRedTop4> : TopState<4> {};
 // kRedLse: online log-sum-exp in base 2 over x = z * (colmul * doc_scale):
 // m = running maximum (starts at the lowest finite float so that masked
 // -inf values never form inf - inf), s = sum 2^((x - m) * log2(e) / tau).
+// Every exponent is <= 0 and the maximum's term is 1, so v_exp_f32 itself
+// serves (exp2f adds a rescaling path for results below 2^-126, which are
+// negligible next to that 1).
+__device__ __forceinline__ float exp2_nonpos(float x) { return __builtin_amdgcn_exp2f(x); }
 template <>
 struct ReducerState<kRedLse> {
   float m, s, k;  // k = colmul * doc_scale of the current target
@@ -118,16 +122,16 @@ struct ReducerState<kRedLse> {
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = z[r] * k;
     const float mn = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-    float acc = s * exp2f((m - mn) * k2);
+    float acc = s * exp2_nonpos((m - mn) * k2);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc += exp2f((x[r] - mn) * k2);
+    for (int r = 0; r < 4; ++r) acc += exp2_nonpos((x[r] - mn) * k2);
     s = acc;
     m = mn;
   }
   __device__ void merge_xor(int mask, float k2) {
     const float mo = __shfl_xor(m, mask), so = __shfl_xor(s, mask);
     const float mn = fmaxf(m, mo);
-    s = s * exp2f((m - mn) * k2) + so * exp2f((mo - mn) * k2);
+    s = s * exp2_nonpos((m - mn) * k2) + so * exp2_nonpos((mo - mn) * k2);
     m = mn;
   }
   __device__ float finish(int len, float, float temperature, float, float) const {
