@@ -340,9 +340,10 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
         // Limb dots combined smallest first; sign documents recover the
         // +-1 dot as 2 (q . bits) - sum(q).
         // int4 documents with three limbs: the two small limbs first as one
-        // exact integer, 254 a1 + a2 (|a| <= 16 * 7 * 127 * 128 < 2^21).
+        // exact integer, 254 a1 + a2 (|a| <= 16 * 7 * 127 * 128 < 2^21, so a
+        // 24-bit multiply is exact).
         auto limbs3 = [&](const v4i (&a)[L][NT]) {
-          const int z12 = a[1 % L][j][rr] * 254 + a[2 % L][j][rr];
+          const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
           return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
         };
         float Y;
