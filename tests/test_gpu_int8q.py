@@ -138,3 +138,29 @@ def test_int8q_scan_partitions_agree_with_oracle(gpu, oracle, scan_partition, le
         top_s, top_i = device.data.topk_batch_int8q(query, 10)
         np.testing.assert_array_equal(top_i, ref_i)
         np.testing.assert_array_equal(top_s, ref_s)
+
+
+@pytest.mark.parametrize("long_len", [4000, 16])
+def test_int8q_scan_one_long_document(gpu, oracle, scan_partition, long_len):
+    """One document far longer than the rest (a wave with thousands of tiles,
+    the tile table's stride set by it) among 600 short ones, including empty
+    documents and documents shorter than a tile; both work splits, scores and
+    the fused top-k bit-exact vs the oracle."""
+    rng = np.random.default_rng(long_len)
+    lengths = rng.integers(0, 40, size=600)
+    lengths[17] = long_len
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    docs = rng.standard_normal((int(offsets[-1]), 128)).astype(np.float32)
+    docs[offsets[17]:offsets[18]] *= 3.0  # the long document is among the best
+    packed = pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    query = np.random.default_rng(5).standard_normal((3, 32, 128)).astype(np.float32)
+    expected = _scores(oracle, packed, query)
+    ref_s, ref_i = oracle.topk(expected, 12)
+    for mode in (0, 1):
+        print(f"case partition={mode} long_len={long_len}", flush=True)
+        scan_partition(mode)
+        device = int4_to_device(packed)
+        np.testing.assert_array_equal(device.data.maxsim_batch_int8q(query), expected)
+        top_s, top_i = device.data.topk_batch_int8q(query, 12)
+        np.testing.assert_array_equal(top_i, ref_i)
+        np.testing.assert_array_equal(top_s, ref_s)
