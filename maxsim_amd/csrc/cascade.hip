@@ -122,10 +122,9 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
                                                            int64_t stride, int64_t m, int64_t* __restrict__ out,
                                                            CandidateTables tab) {
   constexpr int E = kSortMaxRow / 1024;  // positions 4 t .. 4 t + 3 of thread t
-  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_hist[4][256];
   __shared__ uint32_t s_sel[kSortMaxRow];  // the selected positions, for the tables
   __shared__ uint32_t s_wave[16];
-  __shared__ uint32_t s_digit, s_above;
   __shared__ uint32_t s_or[16], s_and[16];
   const int tid = threadIdx.x, lane = tid % kWave;
   const float* row = scores + (int64_t)blockIdx.x * stride;
@@ -150,6 +149,7 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
       kor |= key[e];
       kand &= key[e];
     }
+  for (int i = tid; i < 4 * 256; i += blockDim.x) (&s_hist[0][0])[i] = 0u;
   kor = wave_reduce(kor, [](uint32_t a, uint32_t b) { return a | b; });
   kand = wave_reduce(kand, [](uint32_t a, uint32_t b) { return a & b; });
   if (lane == 0) {
@@ -167,45 +167,49 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
   const int top = diff == 0u ? -1 : 31 - __clz(diff);  // highest varying bit
   uint32_t mask = top >= 31 ? 0u : ~0u << (top + 1);
   uint32_t prefix = kand & mask, need = (uint32_t)m;
-  for (int hi = top; hi >= 0; hi -= 8) {
+  // One histogram per round (at most four rounds of 8 bits), all zeroed
+  // before the reduction's barrier above, and every wave finds the digit
+  // itself from the histogram: one barrier per round.
+  int round = 0;
+  for (int hi = top; hi >= 0; hi -= 8, ++round) {
     const int shift = hi >= 7 ? hi - 7 : 0;
     const uint32_t dmask = (hi - shift == 31 ? ~0u : (2u << (hi - shift)) - 1u);  // digit of bits shift..hi
-    for (int i = tid; i < 256; i += blockDim.x) s_hist[i] = 0;
-    __syncthreads();
+    uint32_t* hist = s_hist[round];
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&s_hist[(key[e] >> shift) & dmask], 1u);
+      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&hist[(key[e] >> shift) & dmask], 1u);
     __syncthreads();
-    if (tid < kWave) {
-      // Lane l holds digits 4l .. 4l + 3; suffix sums over the lanes from
-      // the top digit down find the digit where the count reaches `need`.
-      uint32_t c[4], local = 0;
+    // Lane l holds digits 4l .. 4l + 3; suffix sums over the lanes from the
+    // top digit down find the digit where the count reaches `need` (exactly
+    // one lane finds it).
+    uint32_t c[4], local = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = s_hist[4 * lane + j];
-        local += c[j];
-      }
-      uint32_t suffix = local;  // inclusive: lanes >= this one
-#pragma unroll
-      for (int d = 1; d < kWave; d <<= 1) {
-        const uint32_t y = __shfl_down(suffix, d);
-        if (lane + d < kWave) suffix += y;
-      }
-      uint32_t above = suffix - local;  // digits of higher lanes
-#pragma unroll
-      for (int j = 3; j >= 0; --j) {
-        if (above < need && above + c[j] >= need) {
-          s_digit = (uint32_t)(4 * lane + j);
-          s_above = above;
-        }
-        above += c[j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      c[j] = hist[4 * lane + j];
+      local += c[j];
     }
-    __syncthreads();
-    prefix |= s_digit << shift;
+    uint32_t suffix = local;  // inclusive: lanes >= this one
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t y = __shfl_down(suffix, d);
+      if (lane + d < kWave) suffix += y;
+    }
+    uint32_t above = suffix - local;  // digits of higher lanes
+    uint32_t digit = 0, above_digit = 0;
+    bool found = false;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      if (above < need && above + c[j] >= need) {
+        digit = (uint32_t)(4 * lane + j);
+        above_digit = above;
+        found = true;
+      }
+      above += c[j];
+    }
+    const int src = (int)__builtin_ctzll(__ballot(found));
+    prefix |= (uint32_t)__builtin_amdgcn_readlane((int)digit, src) << shift;
     mask |= dmask << shift;
-    need -= s_above;
-    __syncthreads();
+    need -= (uint32_t)__builtin_amdgcn_readlane((int)above_digit, src);
   }
   // Stable compaction in position order.
   uint32_t eq = 0;
