@@ -101,6 +101,24 @@ def test_weight_shapes(gpu, oracle, shape):
     _close(got, exp)
 
 
+def test_weights_change_between_calls_on_one_handle(gpu, oracle):
+    """The handle keeps the last weight vector on the device and copies a
+    new one only when it differs: alternating weights (including a change of
+    sign of zero only) each give the oracle's scores."""
+    docs, offsets, query, weights, _ = _reducer_fixture()
+    packed, h = _int4_handle(docs, offsets, "token")
+    w2 = weights[::-1].copy()
+    w3 = weights.copy()
+    w3[0, 3] = -0.0
+    for w in (weights, w2, weights, w3, w3, weights):
+        got = h.score_batch(query, reducer="weighted_maxsim", query_weights=w)
+        exp = oracle.int4_fp32_scores(query, packed.values, offsets, token_scale=packed.token_scale,
+                                      reducer="weighted_maxsim", weights=w)
+        _close(got, exp)
+        if w is w3:
+            np.testing.assert_array_equal(np.signbit(got), np.signbit(exp))
+
+
 def test_smoothsim_large_values_stay_finite(gpu):
     docs, offsets, query, _, _ = _reducer_fixture()
     _, h = _int4_handle(docs, offsets, "token")
