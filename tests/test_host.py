@@ -258,3 +258,17 @@ def test_cascade_size_validation(kwargs, match):
     packed = pack_residual_int4(corpus.embeddings, corpus.offsets)
     with pytest.raises(ValueError, match=match):
         cascade_topk(np.ones((2, 128), np.float32), packed, kwargs["k"], candidates=kwargs["candidates"])
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says so
+    (before touching a GPU)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                          timeout=120)
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stderr
