@@ -137,6 +137,23 @@ int msim_int4_maxsim_int8q_async(msim_int4_docs* h, const float* d_query, int64_
 int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
                                int64_t query_tokens, int64_t k, float* d_scores,
                                int64_t* d_indices, void* stream);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): msim_int4_topk_int8q_async with the same arguments and
+ * results, whose scratch memory (quantised query, score rows, the fused
+ * selection's ticket) is a fixed 166,144-byte device array per GPU instead of
+ * handle workspaces, so the call allocates nothing.  Limits: 1 <= batch *
+ * query_tokens <= 128, k <= 32, and either the fused selection applies
+ * (256 <= num_docs <= 4096, batch <= 8, msim_set_fused_topk mode 1 or 2) or
+ * batch * num_docs <= 32768; other sizes fail with MSIM_EINVAL.  The handle's
+ * scan tables are built by msim_int4_create; after msim_set_docs_per_wave or
+ * msim_set_scan_partition changes, one msim_int4_topk_int8q_async call must
+ * rebuild them first.  The first call on a device looks the array up
+ * (make it outside graph capture).  All calls on one GPU share the array:
+ * calls that overlap on one GPU race. */
+int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                 int64_t query_tokens, int64_t k, float* d_scores,
+                                 int64_t* d_indices, void* stream);
 
 /* Stage-level device entry points of the int8-query path (no reference
  * counterpart; the reference fuses them inside launch_int8q_maxsim,

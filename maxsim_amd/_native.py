@@ -44,6 +44,7 @@ SIGNATURES: dict[str, list] = {
     "msim_int4_topk_batch_int8q": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_int4_maxsim_int8q_async": [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp],
     "msim_int4_topk_int8q_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "msim_int4_topk_int8q_noalloc": [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
     "msim_int4_quantize_int8q_async": [c_vp, c_vp, c_i64, c_i64, c_vp],
     "msim_int4_score_int8q_async": [c_vp, c_i64, c_i64, c_vp, c_vp],
     "msim_int4_topk_quantized_async": [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],

@@ -229,6 +229,10 @@ void score_int8q(msim_int4_docs* h, int64_t batch, int64_t query_tokens, float* 
   }
 }
 
+}  // namespace
+
+namespace msim {
+
 // Scan tables of the handle for the requested wave count (cached).
 void build_wave_info(msim_int4_docs* h, int64_t waves) {
   if (h->partition_waves == waves && h->partition_mode == g_scan_partition) return;
@@ -255,6 +259,28 @@ int64_t scan_waves(const msim_int4_docs* h) {
                                       : (int64_t)device_cu_count() * kScanWavesPerCu;
   return std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
 }
+
+bool scan_tables_current(const msim_int4_docs* h) {
+  return h->partition_waves == scan_waves(h) && h->partition_mode == g_scan_partition;
+}
+
+void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a) {
+  a.codes = h->packed.as<uint8_t>();
+  a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
+  a.offsets = h->offsets.as<int64_t>();
+  a.wave_info = h->wave_info.as<int64_t>();
+  a.tile_table = h->tile_table.as<uint64_t>();
+  a.tile_stride = h->tile_stride;
+  a.num_waves = h->num_scan_waves;
+  a.query_tokens = (int32_t)query_tokens;
+  a.scale = h->scale;
+  a.score_stride = h->num_docs;
+  a.num_docs = h->num_docs;
+}
+
+}  // namespace msim
+
+namespace {
 
 // Score the query quantised in the workspace: the MFMA scan for passes of at
 // most 128 query rows, the row-maxima path beyond.
@@ -286,33 +312,16 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     throw InvalidArgument("no quantised query of this shape: call quantize first with the same batch and query_tokens");
   build_wave_info(h, scan_waves(h));
   ScanArgs a{};
-  a.codes = h->packed.as<uint8_t>();
-  a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
-  a.offsets = h->offsets.as<int64_t>();
-  a.wave_info = h->wave_info.as<int64_t>();
-  a.tile_table = h->tile_table.as<uint64_t>();
-  a.tile_stride = h->tile_stride;
-  a.num_waves = h->num_scan_waves;
-  a.query_tokens = (int32_t)query_tokens;
-  a.scale = h->scale;
-  a.score_stride = h->num_docs;
-  a.num_docs = h->num_docs;
+  scan_corpus_args(h, query_tokens, a);
   if (k > 0) {
-    // Fill kernels, not memsets, so that a captured call records no memset
-    // node; both fills run once per allocation.
+    // A fill kernel, not a memset, so that a captured call records no memset
+    // node; it runs once per allocation (the selecting workgroup resets the
+    // ticket).
     if (h->ticket.ptr == nullptr) {
       h->ticket.ensure(256, "hipMalloc scan ticket");
       check_hip(launch_fill_f32(h->ticket.as<float>(), 1, 0.0f, stream), "zero scan ticket");
     }
-    if (h->tail_rows < batch) {
-      h->tail_scores.ensure(sizeof(float) * (size_t)(batch * kScanTailRow), "hipMalloc scan tail rows");
-      h->tail_rows = (int64_t)(h->tail_scores.cap / (sizeof(float) * kScanTailRow));
-      float pad;
-      const uint32_t bits = 0xFFFFFFFFu;
-      std::memcpy(&pad, &bits, sizeof pad);
-      check_hip(launch_fill_f32(h->tail_scores.as<float>(), h->tail_rows * kScanTailRow, pad, stream),
-                "fill scan tail rows");
-    }
+    h->tail_scores.ensure(sizeof(float) * (size_t)(batch * kScanTailRow), "hipMalloc scan tail rows");
     d_scores = h->tail_scores.as<float>();
     a.score_stride = kScanTailRow;
     a.topk_k = (int32_t)k;
@@ -411,6 +420,9 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
       check_hip(hipMemcpy(h->packed.ptr, packed, h->packed_size, hipMemcpyHostToDevice), "copy int4 packed docs to device");
     check_hip(hipMemcpy(h->offsets.ptr, offsets, h->offsets_size * 8, hipMemcpyHostToDevice), "copy int4 offsets to device");
     if (dim < 128) upload_codes128(h->codes128, packed, num_tokens, row_bytes, "int4 packed docs (128 dims)");
+    // The int8-query scan's tables, built here so that the first search (and
+    // msim_int4_topk_int8q_noalloc) finds them resident.
+    if (dim == 128 && h->num_docs > 0) build_wave_info(h.get(), scan_waves(h.get()));
     *out = h.release();
   });
 }

@@ -111,9 +111,8 @@ struct msim_int4_docs {
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
   // Scan with fused top-k: workgroup ticket (zero between launches) and score
-  // rows of kScanTailRow floats, prefilled with the padding bits 0xFFFFFFFF.
+  // rows of kScanTailRow floats.
   msim::DeviceBuffer ticket, tail_scores;
-  int64_t tail_rows = 0;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
@@ -153,3 +152,13 @@ struct msim_binary_docs {
     return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + ws.bytes();
   }
 };
+
+namespace msim {
+// int8-query scan tables of a handle (capi.cpp): build (cached by wave count
+// and partition mode), the wave count the current settings ask for, whether
+// the resident tables match it, and the corpus fields of ScanArgs.
+void build_wave_info(msim_int4_docs* h, int64_t waves);
+int64_t scan_waves(const msim_int4_docs* h);
+bool scan_tables_current(const msim_int4_docs* h);
+void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a);
+}  // namespace msim

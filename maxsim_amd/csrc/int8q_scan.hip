@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   uint64_t* cand = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
   constexpr int kCap = (int)(sizeof(s_codes[0]) / sizeof(uint64_t)) - 1;  // and one spare entry
   for (int b = wave; b < p.batch; b += kScanWaves)
-    tail_topk(scores + (int64_t)b * p.score_stride, p.topk_k, cand, min(kCap, p.tail_cap),
+    tail_topk(scores + (int64_t)b * p.score_stride, (int)p.num_docs, p.topk_k, cand, min(kCap, p.tail_cap),
               p.top_scores + (int64_t)b * p.topk_k,
               p.top_ids + (int64_t)b * p.topk_k);
   if (threadIdx.x == 0) __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

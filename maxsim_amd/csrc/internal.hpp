@@ -81,8 +81,8 @@ struct ScanArgs {
   float* scores;                // [batch, score_stride]
   int64_t score_stride;
   // Fused selection (topk_k > 0): scores are stored write-through into rows
-  // of score_stride = kScanTailRow floats whose columns num_docs and up hold
-  // the bits 0xFFFFFFFF (kScanTailMinDocs <= num_docs <= kScanTailMaxDocs), and the last
+  // of score_stride = kScanTailRow floats (kScanTailMinDocs <= num_docs <=
+  // kScanTailMaxDocs; columns num_docs and up are ignored), and the last
   // workgroup to take a ticket selects the top-k of every batch row into
   // top_scores / top_ids [batch, topk_k], then resets *ticket to 0.
   int32_t topk_k;

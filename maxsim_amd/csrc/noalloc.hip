@@ -1,0 +1,114 @@
+// noalloc.hip -- msim_int4_topk_int8q_noalloc: the int8-query search of
+// msim_int4_topk_int8q_async with its scratch memory (quantised query, score
+// rows, the fused selection's ticket) in one fixed device array instead of
+// handle workspaces, so a call allocates nothing.  For callers that cannot
+// allocate device memory (code under HIP graph capture, tight serving loops).
+//
+// The array `scratch` is a file-scope __device__ object: every GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends.  Host code never names it after set-up: the first call on a device
+// looks its address up with hipGetSymbolAddress (with that device current)
+// and keeps it per device.  Every call on a GPU shares that GPU's array and
+// leaves its contents behind; calls that overlap on one GPU (different
+// streams, or different host threads) race on it.  The ticket is zeroed at
+// set-up and the selecting workgroup resets it at the end of every launch.
+#include <mutex>
+
+#include "capi_handles.hpp"
+
+namespace msim {
+namespace {
+
+constexpr int64_t kNoallocMaxRows = 128;                     // batch * query_tokens per call
+constexpr int64_t kNoallocQueryRows = kNoallocMaxRows + 128;  // padded rows the scan may read
+constexpr int64_t kNoallocScoreFloats = kScanTailMaxRows * kScanTailRow;  // 32,768 scores
+constexpr size_t kQpackOff = 0;
+constexpr size_t kQscaleOff = kQpackOff + kNoallocQueryRows * 128;
+constexpr size_t kQbiasOff = kQscaleOff + kNoallocQueryRows * 4;
+constexpr size_t kScoresOff = kQbiasOff + kNoallocQueryRows * 4;
+constexpr size_t kTicketOff = kScoresOff + kNoallocScoreFloats * 4;
+constexpr size_t kScratchBytes = kTicketOff + 256;  // 166,144 bytes
+static_assert(kScoresOff % 256 == 0 && kTicketOff % 256 == 0, "aligned scratch regions");
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's `scratch`, looked up (and its ticket
+// zeroed on `stream`) at the first call on the device.
+unsigned char* scratch_on(int device, hipStream_t stream) {
+  if (device < 0 || device >= kMaxDevices) throw RuntimeError("device ordinal out of range for the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr) throw RuntimeError("hipGetSymbolAddress(scratch) returned no address");
+    auto* base = static_cast<unsigned char*>(ptr);
+    check_hip(launch_fill_f32(reinterpret_cast<float*>(base + kTicketOff), 1, 0.0f, stream), "zero scratch ticket");
+    g_scratch_ptr[device] = base;
+  }
+  return g_scratch_ptr[device];
+}
+
+}  // namespace
+}  // namespace msim
+
+using namespace msim;
+
+extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_query, int64_t batch,
+                                            int64_t query_tokens, int64_t k, float* d_scores,
+                                            int64_t* d_indices, void* stream) {
+  return guarded([&] {
+    require_handle(h);
+    if (k < 1 || k > h->num_docs) throw InvalidArgument("k must be between 1 and num_docs");
+    if (h->dim != 128) throw InvalidArgument("int8 query scoring currently requires dim=128");
+    require_shape(batch, query_tokens);
+    if (batch == 0) return;
+    const int64_t rows = batch * query_tokens;
+    if (query_tokens == 0 || rows > kNoallocMaxRows)
+      throw InvalidArgument("msim_int4_topk_int8q_noalloc takes 1 to 128 query rows (batch * query_tokens)");
+    if (k > kScanTailMaxK) throw InvalidArgument("msim_int4_topk_int8q_noalloc takes k <= 32");
+    const int64_t n = h->num_docs;
+    const int mode = msim_get_fused_topk();
+    const bool fused =
+        mode != 0 && n >= kScanTailMinDocs && n <= kScanTailMaxDocs && batch <= kScanTailMaxRows;
+    if (!fused && batch * n > kNoallocScoreFloats)
+      throw InvalidArgument(
+          "msim_int4_topk_int8q_noalloc holds batch * num_docs <= 32768 scores unless the scan selects the top-k "
+          "itself (256 <= num_docs <= 4096, batch <= 8)");
+    if (!scan_tables_current(h))
+      throw InvalidArgument(
+          "the scan tables of this handle were built for other partition settings: make one "
+          "msim_int4_topk_int8q_async call to rebuild them");
+    check_hip(hipSetDevice(h->device), "hipSetDevice");
+    const hipStream_t s = as_stream(stream);
+    unsigned char* base = scratch_on(h->device, s);
+    auto* qpack = reinterpret_cast<int8_t*>(base + kQpackOff);
+    auto* qscale = reinterpret_cast<float*>(base + kQscaleOff);
+    auto* qbias = reinterpret_cast<int32_t*>(base + kQbiasOff);
+    auto* scores = reinterpret_cast<float*>(base + kScoresOff);
+    const int64_t rows_padded = ((rows + 15) / 16) * 16 + 128;
+    check_hip(launch_quantize_int8(d_query, rows, rows_padded, qpack, qscale, qbias, s),
+              "launch int8 query quantize kernel");
+    ScanArgs a{};
+    scan_corpus_args(h, query_tokens, a);
+    a.qpack = qpack;
+    a.qscale = qscale;
+    a.batch = (int32_t)batch;
+    a.scores = scores;
+    if (fused) {
+      a.score_stride = kScanTailRow;
+      a.topk_k = (int32_t)k;
+      a.tail_cap = mode == 2 ? 0 : INT32_MAX;
+      a.ticket = reinterpret_cast<uint32_t*>(base + kTicketOff);
+      a.top_scores = d_scores;
+      a.top_ids = d_indices;
+    }
+    check_hip(launch_int8q_scan(a, h->has_token_scale, s), "launch int8q scan kernel");
+    if (!fused)
+      check_hip(launch_topk(scores, batch, n, n, k, nullptr, d_scores, d_indices, s),
+                "launch int8q topk selection kernel");
+  });
+}

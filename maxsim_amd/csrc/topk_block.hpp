@@ -405,10 +405,10 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // ----------------------------------------------------------------- tail form
 // One wave selects the top-k of a row of n <= kTailRow scores that other
 // workgroups of the same launch wrote with agent-scope atomic stores; they are
-// read back with coherent loads.  The row occupies kTailRow floats, positions
-// n and up holding the padding bits 0xFFFFFFFF: their keys are 0, the lowest,
-// and their positions are above every score's, so padding ranks below every
-// score and, as k <= n, is never selected; no element needs a bounds check.
+// read back with coherent loads.  The row occupies kTailRow floats; positions
+// n and up (whatever they hold) get the key 0, the lowest, and their
+// positions are above every score's, so they rank below every score and, as
+// k <= n, are never selected.
 // With T32 the k-th largest of the lanes' maximum 32-bit keys (ties counted;
 // a radix selection by ballots), every key of
 // the top-k is >= T32 and those candidates lie in the (about k) lanes whose
@@ -420,8 +420,6 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // 1 <= k <= 64, 256 <= n (every lane's maximum is a score's, not padding).
 constexpr int kTailEPT = 64;
 constexpr int kTailRow = kTailEPT * kWave;  // 4096
-constexpr uint32_t kTailPadBits = 0xFFFFFFFFu;
-
 __device__ __forceinline__ uint64_t full_key(uint32_t key, uint32_t pos) {
   return ((uint64_t)key << 32) | (0xFFFFFFFFu - pos);
 }
@@ -456,12 +454,12 @@ __device__ __forceinline__ void tail_write(uint64_t key, const float* row, float
 // Not inlined: the caller's registers are free by then, and inlining would
 // let the register allocation of a large caller grow around it.  Arguments
 // arrive in VGPRs; the wave-uniform ones are moved back to SGPRs.
-__device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int k_arg, uint64_t* cand_arg, int cap_arg,
-                                                    float* out_s_arg, int64_t* out_i_arg) {
+__device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_arg, int k_arg, uint64_t* cand_arg,
+                                                    int cap_arg, float* out_s_arg, int64_t* out_i_arg) {
   const float* row = reinterpret_cast<const float*>(wave_uniform64(reinterpret_cast<int64_t>(row_arg)));
   float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
   int64_t* out_i = reinterpret_cast<int64_t*>(wave_uniform64(reinterpret_cast<int64_t>(out_i_arg)));
-  const int k = wave_uniform(k_arg), cap = wave_uniform(cap_arg);
+  const int n = wave_uniform(n_arg), k = wave_uniform(k_arg), cap = wave_uniform(cap_arg);
   // `cand_arg` points into LDS: address it as LDS (ds_* instructions).
   typedef __attribute__((address_space(3))) uint64_t lds_u64;
   lds_u64* cand = (lds_u64*)cand_arg;
@@ -472,7 +470,8 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int k_
   for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
     const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) key[4 * e4 + c] = score_key(__uint_as_float(v[c]));
+    for (int c = 0; c < 4; ++c)
+      key[4 * e4 + c] = tail_pos(4 * e4 + c, lane) < (uint32_t)n ? score_key(__uint_as_float(v[c])) : 0u;
   }
   // T32, the k-th largest of the 64 lanes' maximum keys (ties counted), is
   // at most the row's k-th largest key: the lanes holding the k largest
@@ -546,7 +545,8 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int k_
       const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint64_t f = full_key(score_key(__uint_as_float(v[c])), tail_pos(4 * e4 + c, lane));
+        const uint32_t pos = tail_pos(4 * e4 + c, lane);
+        const uint64_t f = full_key(pos < (uint32_t)n ? score_key(__uint_as_float(v[c])) : 0u, pos);
         best = (f < prev && f > best) ? f : best;
       }
     }
