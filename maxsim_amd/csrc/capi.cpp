@@ -160,11 +160,14 @@ void quantize_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int6
   // Kernels read whole 16-row query tiles, up to 128 rows from a pass's
   // first row; pad (with zero rows) so those reads stay in bounds.
   const int64_t rows_padded = ((rows + 15) / 16) * 16 + 128;
-  h->qpack.ensure(rows_padded * 128, "hipMalloc int8q query codes");
+  // The scan (query_tokens <= 128) reads the codes in lane order, one region
+  // per pass; the row-pass kernel in row order.
+  const int64_t pass_rows = query_tokens <= 128 ? scan_pass_rows(query_tokens) : 0;
+  h->qpack.ensure(std::max<int64_t>(rows_padded * 128, scan_qpack_bytes(rows, pass_rows)), "hipMalloc int8q query codes");
   h->qscale.ensure(rows_padded * 4, "hipMalloc int8q query scales");
   h->qbias.ensure(rows_padded * 4, "hipMalloc int8q query bias");
   check_hip(launch_quantize_int8(d_query, rows, rows_padded, h->qpack.as<int8_t>(),
-                                 h->qscale.as<float>(), h->qbias.as<int32_t>(), stream),
+                                 h->qscale.as<float>(), h->qbias.as<int32_t>(), stream, pass_rows),
             "launch int8 query quantize kernel");
   h->quantized_rows = rows;
 }
@@ -260,6 +263,11 @@ int64_t scan_waves(const msim_int4_docs* h) {
   return std::max<int64_t>(1, std::min<int64_t>(waves, h->num_docs));
 }
 
+int scan_epilogue(const msim_int4_docs* h) {
+  if (!h->has_token_scale) return kScanEpiIntMax;
+  return h->token_scales_fma ? kScanEpiFma : kScanEpiCvt;
+}
+
 bool scan_tables_current(const msim_int4_docs* h) {
   return h->partition_waves == scan_waves(h) && h->partition_mode == g_scan_partition;
 }
@@ -281,13 +289,6 @@ void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a
 }  // namespace msim
 
 namespace {
-
-// Score the query quantised in the workspace: the MFMA scan for passes of at
-// most 128 query rows, the row-maxima path beyond.
-#ifndef MSIM_SCAN_PASS_ROWS
-#define MSIM_SCAN_PASS_ROWS 128
-#endif
-constexpr int64_t kScanPassRows = MSIM_SCAN_PASS_ROWS;  // query rows per scan launch
 
 // The scan selects the top-k itself (last-workgroup tail) when every pass's
 // batch rows and the corpus fit the tail's limits.
@@ -331,7 +332,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
   const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
   for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
     const int64_t nb = std::min(per_pass, batch - b0);
-    a.qpack = h->qpack.as<int8_t>() + b0 * query_tokens * 128;
+    a.qpack = h->qpack.as<int8_t>() + (b0 / per_pass) * scan_qpack_bytes(per_pass * query_tokens, per_pass * query_tokens);
     a.qscale = h->qscale.as<float>() + b0 * query_tokens;
     a.batch = (int32_t)nb;
     a.scores = d_scores + b0 * a.score_stride;
@@ -339,7 +340,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
       a.top_scores = d_top_s + b0 * k;
       a.top_ids = d_top_i + b0 * k;
     }
-    check_hip(launch_int8q_scan(a, h->has_token_scale, stream), "launch int8q scan kernel");
+    check_hip(launch_int8q_scan(a, scan_epilogue(h), stream), "launch int8q scan kernel");
   }
 }
 
@@ -447,6 +448,8 @@ extern "C" int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_s
     // The MFMA kernels multiply 16 * dot by s / 16 (a power-of-two rescale,
     // exact for normal floats).
     upload_scaled(h->token_scales16, token_scales, count, 0.0625f, "int4 token scale vector / 16");
+    h->token_scales_fma = std::all_of(token_scales, token_scales + count,
+                                      [](float v) { return v >= kScanFmaMinScale && v < kScanFmaMaxScale; });
     h->has_token_scale = true;
   });
 }

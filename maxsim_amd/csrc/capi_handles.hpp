@@ -95,6 +95,7 @@ struct msim_int4_docs {
   uint64_t packed_size = 0;
   uint64_t offsets_size = 0;
   bool has_token_scale = false;
+  bool token_scales_fma = false;  // every token scale in [kScanFmaMinScale, kScanFmaMaxScale)
   bool has_residual = false;
   int64_t quantized_rows = -1;  // rows of the query currently quantised in qpack
   int64_t max_doc_tiles = 1;    // 16-token tiles of the longest document
@@ -160,5 +161,6 @@ namespace msim {
 void build_wave_info(msim_int4_docs* h, int64_t waves);
 int64_t scan_waves(const msim_int4_docs* h);
 bool scan_tables_current(const msim_int4_docs* h);
+int scan_epilogue(const msim_int4_docs* h);
 void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a);
 }  // namespace msim

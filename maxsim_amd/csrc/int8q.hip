@@ -12,6 +12,8 @@
 // dot products; the epilogue scales by the token scale (scale before max),
 // keeps a per-lane running max and finishes each document with a
 // cross-lane max and numpy's float64 pairwise sum over query tokens.
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -21,25 +23,59 @@ namespace msim {
 
 // One wave per query row of 128 dims: sigma = f32(max|q| / 127) (0 -> 1),
 // q8 = clip(rint(q / sigma), -127, 127) with a correctly rounded divide.
-// Output row layout (the MFMA B operand order): for lane group g = 0..3,
-// bytes [32g, 32g+16) hold dims 32g+2i (i = 0..15) and bytes
-// [32g+16, 32g+32) hold dims 32g+2i+1 -- the low and high nibbles of the
-// document bytes 16g..16g+15.  bias = -8 * sum(q8) undoes the +8 offset the
-// nibble unpack adds to every document code.
+// bias = -8 * sum(q8) undoes the +8 offset the row-pass kernel's nibble
+// unpack adds to every document code.  Two layouts of the codes (the MFMA B
+// operands):
+//  * row order (pass_rows == 0; the row-pass kernel): row r at r * 128, where
+//    for lane group g = 0..3 bytes [32g, 32g+16) hold dims 32g+2i (i = 0..15)
+//    and bytes [32g+16, 32g+32) dims 32g+2i+1 -- the low and high nibbles of
+//    the document bytes 16g..16g+15;
+//  * lane order (pass_rows > 0; the scan): the rows of scan pass p (rows
+//    [p * pass_rows, (p + 1) * pass_rows)) fill a region of TP = ceil(pass_rows
+//    / 16) tiles of 2 KiB; in tile j the 16 bytes lane (g, c) holds -- row 16j
+//    + c, dims 32g+2i (half 0) or 32g+2i+1 (half 1) -- sit at (2j + half) *
+//    1024 + (16g + c) * 16, so a wave reads each half-tile as one linear
+//    1 KiB run.  Slots of no row hold zeros.
+// Items t < rows_padded also write qscale[t] / qbias[t] (0 past `rows`).
 __global__ __launch_bounds__(256) void quantize_query_int8_kernel(
-    const float* __restrict__ query, int64_t rows, int64_t rows_padded,
+    const float* __restrict__ query, int64_t rows, int64_t rows_padded, int64_t pass_rows, int64_t items,
     int8_t* __restrict__ qpack, float* __restrict__ qscale, int32_t* __restrict__ qbias) {
   const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (row >= rows_padded) return;
-  int8_t* dst = qpack + row * 128;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (t >= items) return;
   const int g = lane >> 4, i = lane & 15;
-  if (row >= rows) {
-    dst[32 * g + i] = 0;
-    dst[32 * g + 16 + i] = 0;
-    if (lane == 0) {
-      qscale[row] = 0.0f;
-      qbias[row] = 0;
+  int64_t row = t;
+  int8_t *dst0 = nullptr, *dst1 = nullptr;  // byte destinations of dims 2 * lane and 2 * lane + 1
+  bool valid = t < rows;
+  if (pass_rows > 0) {
+    const int64_t tp = (pass_rows + 15) / 16;
+    const int64_t slots = ((rows + pass_rows - 1) / pass_rows) * tp * 16;
+    if (t < slots) {
+      const int64_t pass = t / (tp * 16), rl = t % (tp * 16);
+      row = pass * pass_rows + rl;
+      valid = rl < pass_rows && row < rows;
+      int8_t* tile = qpack + (pass * tp + rl / 16) * 2048 + (16 * g + rl % 16) * 16 + i;
+      dst0 = tile;
+      dst1 = tile + 1024;
+    } else {
+      valid = false;
+    }
+    if (t >= rows && t < rows_padded && lane == 0) {
+      qscale[t] = 0.0f;
+      qbias[t] = 0;
+    }
+  } else if (t < rows_padded) {
+    dst0 = qpack + t * 128 + 32 * g + i;
+    dst1 = dst0 + 16;
+    if (!valid && lane == 0) {
+      qscale[t] = 0.0f;
+      qbias[t] = 0;
+    }
+  }
+  if (!valid) {
+    if (dst0 != nullptr) {
+      *dst0 = 0;
+      *dst1 = 0;
     }
     return;
   }
@@ -49,8 +85,8 @@ __global__ __launch_bounds__(256) void quantize_query_int8_kernel(
   const int a = max(-127, min(127, (int)rintf(__fdiv_rn(v.x, s))));
   const int b = max(-127, min(127, (int)rintf(__fdiv_rn(v.y, s))));
   const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
-  dst[32 * g + i] = (int8_t)a;
-  dst[32 * g + 16 + i] = (int8_t)b;
+  *dst0 = (int8_t)a;
+  *dst1 = (int8_t)b;
   if (lane == 0) {
     qscale[row] = s;
     qbias[row] = -8 * sum;
@@ -242,13 +278,20 @@ __global__ __launch_bounds__(256) void int8q_finish_kernel(const float* __restri
 
 // ------------------------------------------------------------------ launch
 
+int64_t scan_qpack_bytes(int64_t rows, int64_t pass_rows) {
+  if (rows <= 0 || pass_rows <= 0) return 0;
+  return ((rows + pass_rows - 1) / pass_rows) * ((pass_rows + 15) / 16) * 2048;
+}
+
 hipError_t launch_quantize_int8(const float* d_query, int64_t rows, int64_t rows_padded,
                                 int8_t* d_qpack, float* d_qscale, int32_t* d_qbias,
-                                hipStream_t stream) {
-  const int64_t blocks = (rows_padded + 3) / 4;
+                                hipStream_t stream, int64_t pass_rows) {
+  const int64_t slots = scan_qpack_bytes(rows, pass_rows) / 128;  // 16 rows per 2 KiB tile
+  const int64_t items = std::max<int64_t>(rows_padded, slots);
+  const int64_t blocks = (items + 3) / 4;
   if (blocks == 0) return hipSuccess;
   quantize_query_int8_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(
-      d_query, rows, rows_padded, d_qpack, d_qscale, d_qbias);
+      d_query, rows, rows_padded, pass_rows, items, d_qpack, d_qscale, d_qbias);
   return hipGetLastError();
 }
 

@@ -137,16 +137,27 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
 #define MSIM_SCAN_OCCUPANCY
 #endif
 
-template <int NT, bool kTS, bool kTail>
+// Epilogue constants of one tile: per accumulator row r (the lane's token
+// 4g + r) the factor a[r] and, for kScanEpiFma, the addend c[r].
+struct TileEpi {
+  float a[4], c[4];
+};
+
+// Bits of 2^23 as an int32: the C operand of a kScanEpiFma tile's first MFMAs.
+constexpr int kMagic = 0x4B000000;
+constexpr int kMaskedAcc = -(1 << 30);  // C operand of masked rows (|16 * dot| < 2^21)
+
+template <int NT, int EPI, bool kTail>
 __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_kernel(
     ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale16,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
     const uint64_t* __restrict__ tile_table, const int8_t* __restrict__ qpack,
     const float* __restrict__ qscale, float* __restrict__ scores) {
+  constexpr bool kTS = EPI != kScanEpiIntMax;
   // LDS: the workgroup's copy of the query tiles; per wave the tile ring
   // (codes as 64 lanes x 16 B, token scales as 64 lanes x 4 B per slot), the
   // per-row maxima of the document being finished and the query scales.
-  constexpr int kQueryParts = (NT + 1) / 2;  // 16-byte loads per lane for the query tiles
+  constexpr int kQueryParts = (NT + 1) / 2;  // 1 KiB half-tiles per wave
   __shared__ __attribute__((aligned(16))) v4u s_query[kQueryParts * kScanWaves * kWave];
   __shared__ __attribute__((aligned(16))) v4u s_codes[kScanWaves][kPrefetch][kWave];
   __shared__ __attribute__((aligned(16))) uint32_t s_scales[kScanWaves][kPrefetch][kWave];
@@ -172,9 +183,10 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
 
   // Global loads, all with an LDS destination (untracked by the compiler,
   // waited for explicitly), in this order: the workgroup's query tiles (each
-  // wave a quarter), this wave's query scales, the first kPrefetch tiles.
+  // wave a quarter of the 1 KiB half-tiles, lane order), this wave's query
+  // scales, the first kPrefetch tiles.
   {
-    const v4i rqp = make_rsrc_words(qpack, (uint32_t)(NT * 16 * 128));
+    const v4i rqp = make_rsrc_words(qpack, (uint32_t)(NT * 2048));
     const uint32_t q_lds = wave_uniform((int)lds_address(s_query));
 #pragma unroll
     for (int i = 0; i < kQueryParts; ++i) {
@@ -215,39 +227,112 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // loads are outstanding; the barrier publishes all four quarters.
   vm_wait_lds<kPrefetch * kOps>();
   __builtin_amdgcn_s_barrier();
-  // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g.
+  // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g; half j
+  // of tile h is the linear 1 KiB run 2j + h (no bank conflicts).
   v4i blo[NT], bhi[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    const v4i* src = reinterpret_cast<const v4i*>(s_query) + (16 * j + c) * 8 + 2 * g;
-    blo[j] = src[0];
-    bhi[j] = src[1];
+    blo[j] = reinterpret_cast<const v4i*>(s_query)[(2 * j) * kWave + lane];
+    bhi[j] = reinterpret_cast<const v4i*>(s_query)[(2 * j + 1) * kWave + lane];
   }
 
-  // Current tile, read back from the ring one step ahead of its use.
-  vm_wait_lds<kRingWait>();
-  v4u w = s_codes[wave][0][lane];
-  v4u sv = kTS ? *reinterpret_cast<const v4u*>(&s_scales[wave][0][0] + 4 * g) : (v4u){0u, 0u, 0u, 0u};
-
+  // Running maxima per query tile: float for the scaled forms, the integer
+  // 16 * dot for tensor-scale corpora.
   float m[NT];
+  int mi[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) m[j] = kNegInf;
-  v4i acc[NT];
-  float sc[4];
+  for (int j = 0; j < NT; ++j) {
+    m[j] = kNegInf;
+    mi[j] = INT32_MIN;
+  }
   constexpr float kInf = __builtin_huge_valf();
 
-  // Epilogue of the tile in acc / sc: running max per query row.  A masked
-  // row has acc = -2^30 + 16 * dot < 0 and scale +inf, i.e. -inf.
-  auto epilogue_max = [&]() {
+  // Epilogue constants and C operand of a tile from its table entry (rows in
+  // bits 32..36 as rows - 1) and its four token scales.  Rows past a short
+  // document are masked: -inf for the scaled forms (c = -inf, or a = +inf on
+  // an accumulator starting at -2^30), a -2^30 start for the integer form.
+  auto prep = [&](uint32_t mhi, const v4u& sv, TileEpi& e) -> v4i {
+    const uint32_t rows = (mhi & 31u) + 1u;
+    v4i cinit = EPI == kScanEpiFma ? (v4i){kMagic, kMagic, kMagic, kMagic} : (v4i){0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const float x0 = (float)acc[j][0] * sc[0];
-      const float x1 = (float)acc[j][1] * sc[1];
-      const float x2 = (float)acc[j][2] * sc[2];
-      const float x3 = (float)acc[j][3] * sc[3];
-      m[j] = max3_op(max3_op(m[j], x0, x1), x2, x3);
+    for (int r = 0; r < 4; ++r) {
+      e.a[r] = kTS ? __uint_as_float(sv[r]) : 0.0625f;
+      e.c[r] = e.a[r] * -8388608.0f;  // -2^23 a, exact
+    }
+    if (rows < 16u) {
+      const uint32_t r0 = 4u * (uint32_t)g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool masked = r0 + (uint32_t)r >= rows;
+        if (EPI == kScanEpiFma) {
+          e.c[r] = masked ? kNegInf : e.c[r];
+        } else {
+          cinit[r] = masked ? kMaskedAcc : 0;
+          if (EPI == kScanEpiCvt) e.a[r] = masked ? kInf : e.a[r];
+        }
+      }
+    }
+    return cinit;
+  };
+  // Half h of the running max over a finished tile's accumulators for query
+  // tile j (accumulator rows 2h, 2h + 1).
+  //  * kScanEpiFma: acc holds the bits of 2^23 + n (n = 16 dot >= 0) or of
+  //    2^23 + n / 2 (n < 0: the binade below 2^23 has half the spacing), so
+  //    fma(F, s/16, -2^23 s/16) is one rounding of dot * s, or of dot * s / 2
+  //    for negative dots; x -> (x >= 0 ? x : x / 2) is increasing, so the
+  //    maximum maps back by min(M, 2M) at the document end.
+  //  * kScanEpiCvt: float(acc) * s/16 (one rounding of dot * s).
+  //  * kScanEpiIntMax: the integer maximum of 16 dot.
+  auto epilogue_half = [&](const v4i& acc, const TileEpi& e, int j, int h) {
+    const int r0 = 2 * h, r1 = 2 * h + 1;
+    if constexpr (EPI == kScanEpiIntMax) {
+      mi[j] = max(max(mi[j], acc[r0]), acc[r1]);
+    } else if constexpr (EPI == kScanEpiFma) {
+      const float x0 = __builtin_fmaf(__int_as_float(acc[r0]), e.a[r0], e.c[r0]);
+      const float x1 = __builtin_fmaf(__int_as_float(acc[r1]), e.a[r1], e.c[r1]);
+      m[j] = max3_op(m[j], x0, x1);
+    } else {
+      const float x0 = (float)acc[r0] * e.a[r0];
+      const float x1 = (float)acc[r1] * e.a[r1];
+      m[j] = max3_op(m[j], x0, x1);
     }
   };
+  // The MFMAs of the next tile (all first halves, then all second halves, so
+  // consecutive MFMAs are independent) interleaved with the epilogue of the
+  // previous one, in a fixed order: each MFMA (16 cycles in the matrix core)
+  // is followed by the VALU instructions of one epilogue half, which read
+  // results of the other accumulator set (no MFMA-to-VALU wait).  The second
+  // halves' operand is unpacked beside the first four groups.
+  auto issue_and_finish = [&](v4i (&acc_q)[NT], const v4u& w_q, const v4i& cinit, const v4i (&acc_p)[NT],
+                              const TileEpi& e_p, bool with_epilogue) {
+    v4i lo, hi;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) lo[x] = (int)((w_q[x] << 4) & 0xF0F0F0F0u);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      acc_q[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+      if (with_epilogue) epilogue_half(acc_p[j], e_p, j, 0);
+      if (j < 4) hi[j] = (int)(w_q[j] & 0xF0F0F0F0u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int x = NT; x < 4; ++x) hi[x] = (int)(w_q[x] & 0xF0F0F0F0u);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      acc_q[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc_q[j], 0, 0, 0);
+      if (with_epilogue) epilogue_half(acc_p[j], e_p, j, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto epilogue = [&](const v4i (&acc)[NT], const TileEpi& e) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      epilogue_half(acc[j], e, j, 0);
+      epilogue_half(acc[j], e, j, 1);
+    }
+  };
+
   // 32-token queries: batch row g is summed by lane group g in registers
   // (tokens c and 16 + c in lane c); its query scales are read once here.
   const bool q32 = NT % 2 == 0 && p.query_tokens == 32;
@@ -260,6 +345,10 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // Document end: per-row maxima over the four lane groups, then the score of
   // local document `local`.
   auto finish = [&](int local) {
+    float mf[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) mf[j] = EPI == kScanEpiIntMax ? (float)mi[j] * 0.0625f : m[j];
+    auto unfold = [](float v) { return EPI == kScanEpiFma ? fminf(v, v + v) : v; };
     if (q32) {
       // numpy's pairwise float64 sum of 32 terms: accumulator k < 8 adds
       // tokens k, k + 8, k + 16, k + 24 in that order (lane k; row_ror:8
@@ -268,7 +357,9 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       // quad 0 then holds the first half, every lane of quad 1 the second)
       // and a half-row mirror (lane 0 reads lane 7).
       float t0, t1;
-      max_scatter_groups<NT>(m, t0, t1);
+      max_scatter_groups<NT>(mf, t0, t1);
+      t0 = unfold(t0);
+      t1 = unfold(t1);
       const double p0 = (double)t0 * (double)sig0, p1 = (double)t1 * (double)sig1;
       double r = __dadd_rn(p0, dpp_f64<0x128>(p0));
       r = __dadd_rn(r, p1);
@@ -277,94 +368,87 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       r = __dadd_rn(r, dpp_f64<0x4E>(r));   // quad_perm [2,3,0,1]
       r = __dadd_rn(r, dpp_f64<0x141>(r));  // row_half_mirror
       if (c == 0 && g < p.batch) put_score(scores + d0 + local + (int64_t)g * p.score_stride, (float)(r * p.scale), fused);
+    } else {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) m[j] = kNegInf;
-      return;
+      for (int j = 0; j < NT; ++j) mf[j] = unfold(max_over_groups(mf[j]));
+      if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = mf[j];
+      }
+      wave_sync_lds();
+      scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride, fused);
+      wave_sync_lds();
     }
 #pragma unroll
-    for (int j = 0; j < NT; ++j) m[j] = max_over_groups(m[j]);
-    if (g == 0) {
-#pragma unroll
-      for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = m[j];
+    for (int j = 0; j < NT; ++j) {
+      m[j] = kNegInf;
+      mi[j] = INT32_MIN;
     }
-    wave_sync_lds();
-    scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride, fused);
-    wave_sync_lds();
-#pragma unroll
-    for (int j = 0; j < NT; ++j) m[j] = kNegInf;
   };
 
-  // Per-tile entries (scalar loads one step ahead): `meta` describes the
-  // tile in `w`, `iss` is the start of the tile kPrefetch steps ahead.
-  uint64_t meta = tt[0], iss = tt[kPrefetch];
-  int slot = 0;
-
-  // One step for tile i (in `w`, ring slot `slot`): refill of that slot,
-  // read-back of the next tile, the tile's MFMAs and its epilogue.  The loop
-  // is bound by instruction issue (an MFMA takes a VALU issue slot).
-  // Measured no faster: MFMAs of tile i interleaved with the epilogue of
-  // tile i - 1 (one or two accumulator sets), accumulators in AGPRs, and a
-  // zero C operand for full tiles (saves the register copies, but the
-  // compiler then interleaves dependent MFMAs with the epilogue).
-  auto step = [&](int i) {
-    v4i lo, hi;
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      hi[x] = (int)(w[x] & 0xF0F0F0F0u);
-      lo[x] = (int)((w[x] << 4) & 0xF0F0F0F0u);
-    }
-    float s0 = 0.0625f, s1 = 0.0625f, s2 = 0.0625f, s3 = 0.0625f;
-    if (kTS) {
-      s0 = __uint_as_float(sv.x);
-      s1 = __uint_as_float(sv.y);
-      s2 = __uint_as_float(sv.z);
-      s3 = __uint_as_float(sv.w);
-    }
-    const uint32_t mhi = (uint32_t)(meta >> 32);
-    const uint32_t rows = (mhi & 31u) + 1u;
-    const bool last = (mhi >> 5) & 1u;
-    const int local = (int)(mhi >> 8);
-    // Rows of a tile past a short document are masked: their accumulators
-    // start at -2^30 (|16 * dot| < 2^22) and their scales are +inf.
-    v4i cinit = (v4i){0, 0, 0, 0};
-    if (rows < 16u) {
-      const uint32_t r0 = 4u * (uint32_t)g;
-      constexpr int kLow = -(1 << 30);
-      cinit = (v4i){r0 + 0u < rows ? 0 : kLow, r0 + 1u < rows ? 0 : kLow, r0 + 2u < rows ? 0 : kLow,
-                    r0 + 3u < rows ? 0 : kLow};
-      s0 = r0 + 0u < rows ? s0 : kInf;
-      s1 = r0 + 1u < rows ? s1 : kInf;
-      s2 = r0 + 2u < rows ? s2 : kInf;
-      s3 = r0 + 3u < rows ? s3 : kInf;
-    }
-    sc[0] = s0;
-    sc[1] = s1;
-    sc[2] = s2;
-    sc[3] = s3;
-    // The slot's contents are in registers before the refill may land.
-    lds_read_done(w, sv);
-    load_tile(slot, (uint32_t)iss);
-    const uint64_t meta_n = tt[i + 1], iss_n = tt[i + 1 + kPrefetch];
-    // Next tile: wait for its slot and read it back (consumed next step).
-    slot = slot + 1 == kPrefetch ? 0 : slot + 1;
+  // Software pipeline over the wave's tiles.  Step i: the MFMAs of tile
+  // i + 1 (raw codes in `w`, scales in `sv`, entry `meta`) go to one
+  // accumulator set while the epilogue of tile i reads the other (its
+  // results are complete: no MFMA-to-VALU wait); the ring slot of tile i + 1
+  // is refilled (tile i + 1 + kPrefetch, starting at token `iss`) and tile
+  // i + 2 is read back from the ring.  Table entries are scalar loads one
+  // step ahead.
+  if (ntiles > 0) {
+    v4i acc_a[NT], acc_b[NT];
+    TileEpi epi_p;       // epilogue constants of the tile whose results are pending
+    uint32_t mhi_p;      // and its table entry (high half)
+    uint64_t meta = tt[0], iss = tt[kPrefetch];
+    int slot = 0;
     vm_wait_lds<kRingWait>();
-    w = s_codes[wave][slot][lane];
-    if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
-    // All first halves, then all second halves: consecutive MFMAs are
-    // independent, so the matrix pipe never waits on its own result.
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc[j], 0, 0, 0);
-    epilogue_max();
-    if (last) finish(local);
-    meta = meta_n;
-    iss = iss_n;
-  };
-
-  // Tile i lives in ring slot i % kPrefetch; the last tile always ends a
-  // document.
-  for (int i = 0; i < ntiles; ++i) step(i);
+    v4u w = s_codes[wave][0][lane];
+    v4u sv = kTS ? *reinterpret_cast<const v4u*>(&s_scales[wave][0][0] + 4 * g) : (v4u){0u, 0u, 0u, 0u};
+    // Read-ahead after tile `slot` left the ring for registers.
+    auto advance = [&](int i_next) {
+      lds_read_done(w, sv);
+      load_tile(slot, (uint32_t)iss);
+      const uint64_t meta_n = tt[i_next], iss_n = tt[i_next + kPrefetch];
+      slot = slot + 1 == kPrefetch ? 0 : slot + 1;
+      vm_wait_lds<kRingWait>();
+      w = s_codes[wave][slot][lane];
+      if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
+      meta = meta_n;
+      iss = iss_n;
+    };
+    // Prologue: tile 0's MFMAs.
+    {
+      mhi_p = (uint32_t)(meta >> 32);
+      const v4i cinit = prep(mhi_p, sv, epi_p);
+      const v4u w_q = w;
+      advance(1);
+      issue_and_finish(acc_a, w_q, cinit, acc_b, epi_p, false);
+    }
+    auto step = [&](int i, v4i (&acc_p)[NT], v4i (&acc_q)[NT]) {
+      const uint32_t mhi_q = (uint32_t)(meta >> 32);
+      TileEpi epi_q;
+      const v4i cinit = prep(mhi_q, sv, epi_q);
+      const v4u w_q = w;
+      advance(i + 2);
+      issue_and_finish(acc_q, w_q, cinit, acc_p, epi_p, true);
+      if ((mhi_p >> 5) & 1u) finish((int)(mhi_p >> 8));
+      mhi_p = mhi_q;
+      epi_p = epi_q;
+    };
+    auto last = [&](const v4i (&acc_p)[NT]) {
+      epilogue(acc_p, epi_p);
+      finish((int)(mhi_p >> 8));  // the last tile always ends a document
+    };
+    int i = 0;
+    for (; i + 2 < ntiles; i += 2) {
+      step(i, acc_a, acc_b);
+      step(i + 1, acc_b, acc_a);
+    }
+    if (i + 1 < ntiles) {
+      step(i, acc_a, acc_b);
+      last(acc_b);
+    } else {
+      last(acc_a);
+    }
+  }
   // No LDS-destination load may still be in flight when the wave ends.
   vm_wait_lds<0>();
 
@@ -397,12 +481,12 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (threadIdx.x == 0) __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool kTS, bool kTail>
+template <int EPI, bool kTail>
 static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_t stream) {
   const dim3 grid((unsigned)blocks), block(kScanThreads);
   switch (nt) {
 #define MSIM_SCAN_CASE(N)                                                                           \
-  int8q_scan_kernel<N, kTS, kTail><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
+  int8q_scan_kernel<N, EPI, kTail><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
                                                         a.wave_info, a.tile_table, a.qpack, a.qscale, \
                                                         a.scores)
     case 1: MSIM_SCAN_CASE(1); break;
@@ -417,10 +501,18 @@ static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_
   }
 }
 
-hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream) {
+template <int EPI>
+static void launch_scan_epi(const ScanArgs& a, int nt, int64_t blocks, bool tail, hipStream_t stream) {
+  if (tail) launch_scan_nt<EPI, true>(a, nt, blocks, stream);
+  else launch_scan_nt<EPI, false>(a, nt, blocks, stream);
+}
+
+hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t stream) {
   const int rows = args.batch * args.query_tokens;
   if (rows <= 0 || rows > 128 || args.num_waves <= 0 || args.num_waves % kScanWaves != 0)
     return hipErrorInvalidValue;
+  if (epilogue != kScanEpiIntMax && epilogue != kScanEpiFma && epilogue != kScanEpiCvt) return hipErrorInvalidValue;
+  if ((epilogue == kScanEpiIntMax) != (args.token_scale16 == nullptr)) return hipErrorInvalidValue;
   if (args.topk_k > 0 &&
       (args.topk_k > kScanTailMaxK || args.topk_k > args.num_docs || args.num_docs > kScanTailMaxDocs ||
        args.num_docs < kScanTailMinDocs || args.score_stride != kTailRow || args.batch > kScanTailMaxRows ||
@@ -430,12 +522,10 @@ hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;
   const bool tail = args.topk_k > 0;
-  if (token_scale) {
-    if (tail) launch_scan_nt<true, true>(args, nt, blocks, stream);
-    else launch_scan_nt<true, false>(args, nt, blocks, stream);
-  } else {
-    if (tail) launch_scan_nt<false, true>(args, nt, blocks, stream);
-    else launch_scan_nt<false, false>(args, nt, blocks, stream);
+  switch (epilogue) {
+    case kScanEpiIntMax: launch_scan_epi<kScanEpiIntMax>(args, nt, blocks, tail, stream); break;
+    case kScanEpiFma: launch_scan_epi<kScanEpiFma>(args, nt, blocks, tail, stream); break;
+    default: launch_scan_epi<kScanEpiCvt>(args, nt, blocks, tail, stream); break;
   }
   return hipGetLastError();
 }

@@ -28,9 +28,15 @@ struct Int8qArgs {
   int32_t rows_valid;
 };
 
+// Quantises rows x 128 fp32 query rows: qscale / qbias [rows_padded] (zero
+// past rows) and the codes in the row-pass kernel's row order (pass_rows ==
+// 0, rows_padded rows) or the scan's lane order (pass_rows > 0: per scan pass
+// of pass_rows rows a region of ceil(pass_rows / 16) tiles of 2 KiB,
+// scan_qpack_bytes in all).
 hipError_t launch_quantize_int8(const float* d_query, int64_t rows, int64_t rows_padded,
                                 int8_t* d_qpack, float* d_qscale, int32_t* d_qbias,
-                                hipStream_t stream);
+                                hipStream_t stream, int64_t pass_rows = 0);
+int64_t scan_qpack_bytes(int64_t rows, int64_t pass_rows);
 hipError_t launch_int8q_maxsim(const Int8qArgs& args, int rows_in_pass, bool token_scale,
                                bool finish, hipStream_t stream);
 hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int64_t batch,
@@ -97,7 +103,21 @@ constexpr int64_t kScanTailMaxDocs = 4096;
 constexpr int64_t kScanTailMinDocs = 256;  // every lane of the selecting wave holds a score
 constexpr int64_t kScanTailRow = 4096;  // floats per score row of the fused selection
 constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
-hipError_t launch_int8q_scan(const ScanArgs& args, bool token_scale, hipStream_t stream);
+// Epilogue forms of the scan (the token scales decide which is exact):
+//  * kScanEpiIntMax: tensor-scale corpora (token_scale16 == nullptr): integer
+//    maximum of the dots, scaled at the document end;
+//  * kScanEpiFma: every token scale s in [2^-122, 2^109): one fma per
+//    element on accumulators offset by 2^23 (int8q_scan.hip);
+//  * kScanEpiCvt: any other positive finite token scales: float(dot) * s.
+enum : int { kScanEpiIntMax = 0, kScanEpiFma = 1, kScanEpiCvt = 2 };
+constexpr float kScanFmaMinScale = 0x1p-122f, kScanFmaMaxScale = 0x1p109f;
+hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t stream);
+// Query rows of one scan launch: whole batch rows, at most 128 rows (one
+// batch row of more than 128 tokens goes to the row-pass kernel instead).
+constexpr int64_t kScanPassRows = 128;
+inline int64_t scan_pass_rows(int64_t query_tokens) {
+  return query_tokens <= 0 ? 0 : (query_tokens >= kScanPassRows ? 1 : kScanPassRows / query_tokens) * query_tokens;
+}
 // Builds the wave table and tile table for `waves` requested waves (the
 // result may hold more rows: ranges are split at kScanMaxDocsPerWave
 // documents and 2^25 tokens, and padded to whole workgroups).  Each wave's

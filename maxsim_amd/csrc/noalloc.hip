@@ -90,7 +90,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
     auto* qbias = reinterpret_cast<int32_t*>(base + kQbiasOff);
     auto* scores = reinterpret_cast<float*>(base + kScoresOff);
     const int64_t rows_padded = ((rows + 15) / 16) * 16 + 128;
-    check_hip(launch_quantize_int8(d_query, rows, rows_padded, qpack, qscale, qbias, s),
+    check_hip(launch_quantize_int8(d_query, rows, rows_padded, qpack, qscale, qbias, s, scan_pass_rows(query_tokens)),
               "launch int8 query quantize kernel");
     ScanArgs a{};
     scan_corpus_args(h, query_tokens, a);
@@ -106,7 +106,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
       a.top_scores = d_scores;
       a.top_ids = d_indices;
     }
-    check_hip(launch_int8q_scan(a, h->has_token_scale, s), "launch int8q scan kernel");
+    check_hip(launch_int8q_scan(a, scan_epilogue(h), s), "launch int8q scan kernel");
     if (!fused)
       check_hip(launch_topk(scores, batch, n, n, k, nullptr, d_scores, d_indices, s),
                 "launch int8q topk selection kernel");

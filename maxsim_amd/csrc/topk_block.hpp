@@ -435,6 +435,11 @@ __device__ __forceinline__ uint32_t tail_pos(int e, int lane) {
   return (uint32_t)(4 * ((e >> 2) * kWave + lane) + (e & 3));
 }
 
+// All ones when element e of the lane lies before position n, else zero.
+__device__ __forceinline__ uint32_t tail_keep(int e, int lane, int n) {
+  return 0u - (uint32_t)(tail_pos(e, lane) < (uint32_t)n);
+}
+
 // Loads carry the agent-scope coherence bit (sc1), as an agent-scope atomic
 // load does.
 __device__ __forceinline__ v4u tail_load(__amdgpu_buffer_rsrc_t rs, int e4, int lane) {
@@ -465,13 +470,17 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_
   lds_u64* cand = (lds_u64*)cand_arg;
   const int lane = lane_id();
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(row, (uint32_t)kTailRow * 4u);
+  // All loads first, then the keys (a position past n keeps the key 0 by
+  // masking, not by a branch, so that no load waits for another).
+  v4u raw[kTailEPT / 4];
+#pragma unroll
+  for (int e4 = 0; e4 < kTailEPT / 4; ++e4) raw[e4] = tail_load(rs, e4, lane);
   uint32_t key[kTailEPT];
 #pragma unroll
   for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
-    const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      key[4 * e4 + c] = tail_pos(4 * e4 + c, lane) < (uint32_t)n ? score_key(__uint_as_float(v[c])) : 0u;
+      key[4 * e4 + c] = score_key(__uint_as_float(raw[e4][c])) & tail_keep(4 * e4 + c, lane, n);
   }
   // T32, the k-th largest of the 64 lanes' maximum keys (ties counted), is
   // at most the row's k-th largest key: the lanes holding the k largest
@@ -545,8 +554,8 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_
       const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint32_t pos = tail_pos(4 * e4 + c, lane);
-        const uint64_t f = full_key(pos < (uint32_t)n ? score_key(__uint_as_float(v[c])) : 0u, pos);
+        const uint64_t f = full_key(score_key(__uint_as_float(v[c])) & tail_keep(4 * e4 + c, lane, n),
+                                    tail_pos(4 * e4 + c, lane));
         best = (f < prev && f > best) ? f : best;
       }
     }
