@@ -131,11 +131,8 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
   }
 }
 
-#ifdef MSIM_SCAN_WAVES_PER_EU
-#define MSIM_SCAN_OCCUPANCY __attribute__((amdgpu_waves_per_eu(MSIM_SCAN_WAVES_PER_EU, MSIM_SCAN_WAVES_PER_EU)))
-#else
-#define MSIM_SCAN_OCCUPANCY
-#endif
+// Two waves per SIMD (eight per CU): at most 256 VGPRs per wave.
+#define MSIM_SCAN_OCCUPANCY __attribute__((amdgpu_waves_per_eu(2, 2)))
 
 // Epilogue constants of one tile: per accumulator row r (the lane's token
 // 4g + r) the factor a[r] and, for kScanEpiFma, the addend c[r].
@@ -473,7 +470,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (s_last == 0) return;
   // Wave w selects batch rows w, w + 4, ...; its tile ring holds the candidates.
   uint64_t* cand = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
-  constexpr int kCap = (int)(sizeof(s_codes[0]) / sizeof(uint64_t)) - 1;  // and one spare entry
+  constexpr int kCap = (int)(sizeof(s_codes[0]) / sizeof(uint64_t)) - kWave;  // and a spare entry per lane
   for (int b = wave; b < p.batch; b += kScanWaves)
     tail_topk(scores + (int64_t)b * p.score_stride, (int)p.num_docs, p.topk_k, cand, min(kCap, p.tail_cap),
               p.top_scores + (int64_t)b * p.topk_k,

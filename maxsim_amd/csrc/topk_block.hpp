@@ -73,13 +73,20 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return v;
 }
 
+// Inclusive prefix sum over the wave: DPP row shifts by 1, 2, 4 and 8 (zero
+// filled at row starts) sum within each row of 16 lanes, then row_bcast:15
+// adds the last lane of rows 0 / 2 to rows 1 / 3 and row_bcast:31 the last
+// lane of row 1 to rows 2 and 3.
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t o = (uint32_t)__shfl_up((int)v, off);
-    if (lane >= off) v += o;
-  }
+  auto shr = [](uint32_t x, auto ctrl) -> uint32_t {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, decltype(ctrl)::value, 0xF, 0xF, true);
+  };
+  v += shr(v, std::integral_constant<int, 0x111>{});  // row_shr:1
+  v += shr(v, std::integral_constant<int, 0x112>{});  // row_shr:2
+  v += shr(v, std::integral_constant<int, 0x114>{});  // row_shr:4
+  v += shr(v, std::integral_constant<int, 0x118>{});  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
   return v;
 }
 
@@ -405,21 +412,38 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // ----------------------------------------------------------------- tail form
 // One wave selects the top-k of a row of n <= kTailRow scores that other
 // workgroups of the same launch wrote with agent-scope atomic stores; they are
-// read back with coherent loads.  The row occupies kTailRow floats; positions
-// n and up (whatever they hold) get the key 0, the lowest, and their
-// positions are above every score's, so they rank below every score and, as
-// k <= n, are never selected.
-// With T32 the k-th largest of the lanes' maximum 32-bit keys (ties counted;
-// a radix selection by ballots), every key of
-// the top-k is >= T32 and those candidates lie in the (about k) lanes whose
-// maximum reaches T32.  They go to `cand` (wave-private LDS of at least
-// cap + 1 entries) with their 64-bit keys (order-preserving score bits above
-// the inverted position, unique) and are ranked by counting.  More than
-// `cap` candidates (the best scores crowded into few lanes, or many ties;
-// cap = 0 forces it) fall back to k rounds of a wave maximum over the row.
+// read back with coherent loads (64 per lane, all issued first).
+//
+// Keys: tail_key maps a float's bits to a 32-bit order-preserving key (u ^
+// 2^31 for sign bit 0, -u otherwise, so -0 ties +0) and full keys put the
+// inverted position below it, so a larger full key is a higher score or, on
+// a tie, a lower position (the reference order).  Positions n and up get the
+// key 0, below every score's, and as k <= n are never selected.
+//
+// T, the k-th largest of the 64 lane maxima (ties counted; a bitonic sort
+// across the wave), is at most the row's k-th largest key: every key of the
+// top-k is >= T.  Candidates (keys >= T) are counted per lane; a lane with
+// one candidate holds exactly its maximum, at the position recorded in the
+// counting pass, and writes it to `cand` at its prefix-sum slot; lanes with
+// more (ties, or the best scores crowded into one lane) store theirs in
+// order in `cand` too (a second pass over the row, taken only then).  The
+// candidates (cap at most, `cand` wave-private LDS of cap + 64 entries) are
+// ranked by counting.  More than cap candidates (cap = 0 forces it) fall
+// back to k rounds of a wave maximum over the row.
 // 1 <= k <= 64, 256 <= n (every lane's maximum is a score's, not padding).
 constexpr int kTailEPT = 64;
 constexpr int kTailRow = kTailEPT * kWave;  // 4096
+
+__device__ __forceinline__ uint32_t tail_key(uint32_t u) {
+  const uint32_t s = (uint32_t)((int32_t)u >> 31);
+  return (u ^ (s | 0x80000000u)) - s;
+}
+
+// The float of a tail key (+0 for the key of +0 and -0).
+__device__ __forceinline__ float tail_key_score(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : (0u - k));
+}
+
 __device__ __forceinline__ uint64_t full_key(uint32_t key, uint32_t pos) {
   return ((uint64_t)key << 32) | (0xFFFFFFFFu - pos);
 }
@@ -435,31 +459,57 @@ __device__ __forceinline__ uint32_t tail_pos(int e, int lane) {
   return (uint32_t)(4 * ((e >> 2) * kWave + lane) + (e & 3));
 }
 
-// All ones when element e of the lane lies before position n, else zero.
-__device__ __forceinline__ uint32_t tail_keep(int e, int lane, int n) {
-  return 0u - (uint32_t)(tail_pos(e, lane) < (uint32_t)n);
-}
-
 // Loads carry the agent-scope coherence bit (sc1), as an agent-scope atomic
 // load does.
 __device__ __forceinline__ v4u tail_load(__amdgpu_buffer_rsrc_t rs, int e4, int lane) {
   return __builtin_amdgcn_raw_buffer_load_b128(rs, (e4 * kWave + lane) * 16, 0, kCoherentLoadPolicy);
 }
 
-// The score of a key (+0 and -0 share one: read back from the row).
+// The score and position of a full key (+0 and -0 share one key: the score
+// is read back from the row).
 __device__ __forceinline__ void tail_write(uint64_t key, const float* row, float* out_s, int64_t* out_i) {
   const uint32_t k32 = (uint32_t)(key >> 32);
   const uint32_t pos = 0xFFFFFFFFu - (uint32_t)key;
-  float s = __uint_as_float((k32 & 0x80000000u) ? (k32 & 0x7FFFFFFFu) : ~k32);
+  float s = tail_key_score(k32);
   if (k32 == 0x80000000u) s = load_score<true>(row + pos);
   *out_s = s;
   *out_i = (int64_t)pos;
 }
 
-// Not inlined: the caller's registers are free by then, and inlining would
-// let the register allocation of a large caller grow around it.  Arguments
-// arrive in VGPRs; the wave-uniform ones are moved back to SGPRs.
-__device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_arg, int k_arg, uint64_t* cand_arg,
+// Descending bitonic sort of one 32-bit value per lane across the wave: DPP
+// exchanges for lane distances 1, 2, 4 and 8, ds_swizzle for 16, a
+// bpermute for 32.
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+  const int lane = lane_id();
+  auto partner = [&](uint32_t x, int d) -> uint32_t {
+    switch (d) {
+      case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+      case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+      case 4: {
+        // lanes with bit 2 clear (banks 0, 2) read l + 4, the others l - 4
+        const int t = __builtin_amdgcn_update_dpp(0, (int)x, 0x104, 0xF, 0x5, false);  // row_shl:4
+        return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)x, 0x114, 0xF, 0xA, false);  // row_shr:4
+      }
+      case 8: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
+      case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F);  // xor 16 within each half
+      default: return (uint32_t)__shfl_xor((int)x, 32);
+    }
+  };
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+    for (int d = size >> 1; d > 0; d >>= 1) {
+      const uint32_t p = partner(v, d);
+      const bool keep_max = ((lane & d) == 0) == ((lane & size) == 0);
+      v = keep_max ? max(v, p) : min(v, p);
+    }
+  }
+  return v;
+}
+
+// Inlined into the calling kernel, whose main-loop registers are dead by
+// then (a call would save the callee-saved registers it uses to scratch).
+__device__ __forceinline__ void tail_topk(const float* row_arg, int n_arg, int k_arg, uint64_t* cand_arg,
                                                     int cap_arg, float* out_s_arg, int64_t* out_i_arg) {
   const float* row = reinterpret_cast<const float*>(wave_uniform64(reinterpret_cast<int64_t>(row_arg)));
   float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
@@ -470,60 +520,46 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_
   lds_u64* cand = (lds_u64*)cand_arg;
   const int lane = lane_id();
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(row, (uint32_t)kTailRow * 4u);
-  // All loads first, then the keys (a position past n keeps the key 0 by
-  // masking, not by a branch, so that no load waits for another).
-  v4u raw[kTailEPT / 4];
-#pragma unroll
-  for (int e4 = 0; e4 < kTailEPT / 4; ++e4) raw[e4] = tail_load(rs, e4, lane);
   uint32_t key[kTailEPT];
 #pragma unroll
   for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
+    const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      key[4 * e4 + c] = score_key(__uint_as_float(raw[e4][c])) & tail_keep(4 * e4 + c, lane, n);
+    for (int c = 0; c < 4; ++c) key[4 * e4 + c] = tail_key(v[c]);
   }
-  // T32, the k-th largest of the 64 lanes' maximum keys (ties counted), is
-  // at most the row's k-th largest key: the lanes holding the k largest
-  // maxima hold k keys >= T32.  Every key >= T32 is a candidate.
+  if (n < kTailRow) {
+#pragma unroll
+    for (int e = 0; e < kTailEPT; ++e) key[e] = tail_pos(e, lane) < (uint32_t)n ? key[e] : 0u;
+  }
   uint32_t mkey = 0;
 #pragma unroll
-  for (int e = 0; e < kTailEPT; ++e) mkey = max(mkey, key[e]);
-  // Radix selection over the 64 lane maxima, one bit per step from the top:
-  // the k-th largest has bit b set iff at least `need` of the lanes matching
-  // the bits chosen so far have it set (ballot + popcount, no LDS).
-  uint32_t t32 = 0, fixed = 0;
-  int need = k;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t bit = 1u << b;
-    const bool match = (mkey & fixed) == t32;
-    const int ones = __builtin_popcountll(__ballot(match && (mkey & bit) != 0));
-    if (ones >= need) t32 |= bit;
-    else need -= ones;
-    fixed |= bit;
-  }
+  for (int e = 0; e < kTailEPT; e += 2) mkey = max(max(mkey, key[e]), key[e + 1]);
+  const uint32_t t = (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(mkey), k - 1);
 
-  // Candidate bitmask of the lane (bit e: key[e] >= t32); a candidate's slot
-  // is the lane's base plus the candidates before it, so the stores do not
-  // depend on each other.
-  uint32_t mlo = 0, mhi = 0;
+  // Candidates per lane, and the element index of the lane's last candidate
+  // (its only one when it has one).
+  int cnt = 0, last = 0;
 #pragma unroll
   for (int e = 0; e < kTailEPT; ++e) {
-    if (e < 32) mlo |= key[e] >= t32 ? 1u << e : 0u;
-    else mhi |= key[e] >= t32 ? 1u << (e - 32) : 0u;
+    const bool take = key[e] >= t;
+    cnt += take ? 1 : 0;
+    last = take ? e : last;
   }
-  const int cnt = __builtin_popcount(mlo) + __builtin_popcount(mhi);
   const int incl = (int)wave_inclusive_scan((uint32_t)cnt);
   const int total = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= k
   if (total <= cap) {
-    // Unconditional stores: a non-candidate goes to the spare entry `cap`.
-    const int base = incl - cnt;
-    if (cnt > 0) {
+    if (cnt == 1) cand[incl - 1] = full_key(mkey, tail_pos(last, lane));
+    if (__ballot(cnt > 1) != 0) {
+      // Lanes with several candidates store them all, in position order.
+      if (cnt > 1) {
+        int slot = incl - cnt;
+        const int spare = cap + lane;
 #pragma unroll
-      for (int e = 0; e < kTailEPT; ++e) {
-        const bool take = e < 32 ? ((mlo >> e) & 1u) != 0 : ((mhi >> (e - 32)) & 1u) != 0;
-        const int before = e < 32 ? __builtin_popcount(mlo & ((1u << e) - 1u))
-                                  : __builtin_popcount(mlo) + __builtin_popcount(mhi & ((1u << (e - 32)) - 1u));
-        cand[take ? base + before : cap] = full_key(key[e], tail_pos(e, lane));
+        for (int e = 0; e < kTailEPT; ++e) {
+          const bool take = key[e] >= t;
+          cand[take ? slot : spare] = full_key(key[e], tail_pos(e, lane));
+          slot += take ? 1 : 0;
+        }
       }
     }
     wave_sync_lds();
@@ -538,14 +574,15 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_
       for (int s = lane; s < total; s += kWave) {
         const uint64_t x = cand[s];
         int r = 0;
-        for (int t = 0; t < total; ++t) r += cand[t] > x ? 1 : 0;
+        for (int q = 0; q < total; ++q) r += cand[q] > x ? 1 : 0;
         if (r < k) tail_write(x, row, out_s + r, out_i + r);
       }
     }
     wave_sync_lds();
     return;
   }
-  // k rounds over the row: the largest key below the previous round's.
+  // k rounds over the row (read again each round): the largest full key
+  // below the previous round's.
   uint64_t prev = ~0ull;
   for (int r = 0; r < k; ++r) {
     uint64_t best = 0;
@@ -554,8 +591,8 @@ __device__ __attribute__((noinline)) void tail_topk(const float* row_arg, int n_
       const v4u v = tail_load(rs, e4, lane);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint64_t f = full_key(score_key(__uint_as_float(v[c])) & tail_keep(4 * e4 + c, lane, n),
-                                    tail_pos(4 * e4 + c, lane));
+        const uint32_t pos = tail_pos(4 * e4 + c, lane);
+        const uint64_t f = full_key(pos < (uint32_t)n ? tail_key(v[c]) : 0u, pos);
         best = (f < prev && f > best) ? f : best;
       }
     }
