@@ -274,7 +274,9 @@ bool scan_tables_current(const msim_int4_docs* h) {
 
 void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a) {
   a.codes = h->packed.as<uint8_t>();
-  a.token_scale16 = h->has_token_scale ? h->token_scales16.as<float>() : nullptr;
+  const int epi = scan_epilogue(h);
+  a.token_scale16 = epi == kScanEpiIntMax ? nullptr
+                    : (epi == kScanEpiFma ? h->token_scales16.as<float>() : h->token_scales.as<float>());
   a.offsets = h->offsets.as<int64_t>();
   a.wave_info = h->wave_info.as<int64_t>();
   a.tile_table = h->tile_table.as<uint64_t>();

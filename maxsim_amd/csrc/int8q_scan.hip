@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     v4i cinit = EPI == kScanEpiFma ? (v4i){kMagic, kMagic, kMagic, kMagic} : (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      e.a[r] = kTS ? __uint_as_float(sv[r]) : 0.0625f;
+      e.a[r] = kTS ? __uint_as_float(sv[r]) : 1.0f;
       e.c[r] = e.a[r] * -8388608.0f;  // -2^23 a, exact
     }
     if (rows < 16u) {
@@ -278,7 +278,8 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   //    fma(F, s/16, -2^23 s/16) is one rounding of dot * s, or of dot * s / 2
   //    for negative dots; x -> (x >= 0 ? x : x / 2) is increasing, so the
   //    maximum maps back by min(M, 2M) at the document end.
-  //  * kScanEpiCvt: float(acc) * s/16 (one rounding of dot * s).
+  //  * kScanEpiCvt: float(acc >> 4) * s (acc = 16 dot exactly; the token
+  //    scales themselves, so one rounding of dot * s for any positive s).
   //  * kScanEpiIntMax: the integer maximum of 16 dot.
   auto epilogue_half = [&](const v4i& acc, const TileEpi& e, int j, int h) {
     const int r0 = 2 * h, r1 = 2 * h + 1;
@@ -289,8 +290,8 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       const float x1 = __builtin_fmaf(__int_as_float(acc[r1]), e.a[r1], e.c[r1]);
       m[j] = max3_op(m[j], x0, x1);
     } else {
-      const float x0 = (float)acc[r0] * e.a[r0];
-      const float x1 = (float)acc[r1] * e.a[r1];
+      const float x0 = (float)(acc[r0] >> 4) * e.a[r0];
+      const float x1 = (float)(acc[r1] >> 4) * e.a[r1];
       m[j] = max3_op(m[j], x0, x1);
     }
   };

@@ -73,7 +73,8 @@ constexpr int kScanWavesPerCu = MSIM_SCAN_WAVES_PER_CU;  // scan waves launched 
 constexpr uint32_t kScanPastEnd = 0x3FFFFF0u;      // (kScanPastEnd + 15) * 64 + 48 < 2^32
 struct ScanArgs {
   const uint8_t* codes;         // [num_tokens, 64] int4 nibbles
-  const float* token_scale16;   // [num_tokens] token scales / 16, or nullptr (tensor scale)
+  const float* token_scale16;   // [num_tokens] token scales / 16 (kScanEpiFma), the token scales
+                                //   themselves (kScanEpiCvt), or nullptr (tensor scale)
   const int64_t* offsets;       // [num_docs + 1]
   const int64_t* wave_info;     // [num_waves, kWaveInfoWords]
   const uint64_t* tile_table;   // per-wave tile entries, wave w's at w * tile_stride
@@ -108,7 +109,8 @@ constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
 //    maximum of the dots, scaled at the document end;
 //  * kScanEpiFma: every token scale s in [2^-122, 2^109): one fma per
 //    element on accumulators offset by 2^23 (int8q_scan.hip);
-//  * kScanEpiCvt: any other positive finite token scales: float(dot) * s.
+//  * kScanEpiCvt: any other positive finite token scales: float(dot) * s
+//    (token_scale16 then holds the scales themselves).
 enum : int { kScanEpiIntMax = 0, kScanEpiFma = 1, kScanEpiCvt = 2 };
 constexpr float kScanFmaMinScale = 0x1p-122f, kScanFmaMaxScale = 0x1p109f;
 hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t stream);

@@ -164,3 +164,27 @@ def test_int8q_scan_one_long_document(gpu, oracle, scan_partition, long_len):
         top_s, top_i = device.data.topk_batch_int8q(query, 12)
         np.testing.assert_array_equal(top_i, ref_i)
         np.testing.assert_array_equal(top_s, ref_s)
+
+
+@pytest.mark.parametrize("factor", [2.0 ** -120, 2.0 ** 115])
+def test_int8q_token_scales_outside_fma_range(gpu, oracle, factor):
+    """The scan's one-fma epilogue needs every token scale in [2^-122, 2^109);
+    a corpus with scales outside it (here every seventh token's scale times
+    2^-120 or 2^115) takes float(dot) * s instead.  Scores and the fused
+    top-k stay bit-exact against the oracle."""
+    import dataclasses
+
+    docs, offsets = ragged_fixture(400, seed=13, lo=0, hi=40)
+    packed = pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    scales = packed.token_scale.copy()
+    scales[::7] *= np.float32(factor)
+    assert np.all(np.isfinite(scales)) and np.all(scales > 0)
+    packed = dataclasses.replace(packed, token_scale=scales)
+    query = np.random.default_rng(17).standard_normal((4, 32, 128)).astype(np.float32)
+    device = int4_to_device(packed)
+    expected = _scores(oracle, packed, query)
+    np.testing.assert_array_equal(device.data.maxsim_batch_int8q(query), expected)
+    top_s, top_i = device.data.topk_batch_int8q(query, 10)
+    ref_s, ref_i = oracle.topk(expected, 10)
+    np.testing.assert_array_equal(top_i, ref_i)
+    np.testing.assert_array_equal(top_s, ref_s)
