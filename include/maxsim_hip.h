@@ -131,7 +131,10 @@ int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query, int64_t ba
                                float* out_scores, int64_t* out_indices);
 /* Device-resident forms of the two calls above: d_query, d_out, d_scores,
  * d_indices are device pointers; work is enqueued on `stream` (a
- * hipStream_t, NULL = default stream) and not waited for. */
+ * hipStream_t, NULL = default stream) and not waited for.  Every *_async
+ * entry point may allocate its workspaces (hipMalloc) and upload tables on
+ * the first call with a given shape; a call under HIP graph capture needs an
+ * earlier call with the same shapes (or msim_int4_topk_int8q_noalloc). */
 int msim_int4_maxsim_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
                                  int64_t query_tokens, float* d_out, void* stream);
 int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,

@@ -24,6 +24,19 @@ T* upload_vec(DeviceBuffer& buf, const std::vector<T>& v, const char* what) {
   return buf.as<T>();
 }
 
+// The same, enqueued on `stream`: a per-call table (weights, candidate
+// tables) is overwritten only after the kernels queued before it on that
+// stream, which may still read the previous call's contents.  From pageable
+// host memory the runtime stages or copies before returning, so `v` may go
+// out of scope afterwards.
+template <typename T>
+T* upload_vec(DeviceBuffer& buf, const std::vector<T>& v, const char* what, hipStream_t stream) {
+  buf.ensure(std::max<size_t>(sizeof(T) * v.size(), sizeof(T)), what);
+  if (!v.empty())
+    check_hip(hipMemcpyAsync(buf.ptr, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, stream), what);
+  return buf.as<T>();
+}
+
 }  // namespace
 
 CandidateLayout candidate_layout(int64_t batch, int64_t query_tokens, int limbs, int64_t per_target,
@@ -86,7 +99,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
         std::memcmp(w.data(), ws.weights_host.data(), sizeof(float) * w.size()) == 0) {
       d_weights = ws.weights.as<float>();
     } else {
-      d_weights = upload_vec(ws.weights, w, "copy reducer query weights to device");
+      d_weights = upload_vec(ws.weights, w, "copy reducer query weights to device", stream);
       ws.weights_host = std::move(w);
     }
   }
@@ -124,8 +137,8 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
       std::vector<int64_t> info;
       std::vector<uint64_t> tiles;
       build_score_tables(off.data(), nullptr, num_docs, waves, info, tiles);
-      upload_vec(ws.full_info, info, "copy score wave table to device");
-      upload_vec(ws.full_tiles, tiles, "copy score tile table to device");
+      upload_vec(ws.full_info, info, "copy score wave table to device", stream);
+      upload_vec(ws.full_tiles, tiles, "copy score tile table to device", stream);
       ws.full_key = waves;
       ws.full_waves = (int64_t)info.size() / kScoreInfoWords;
     }
@@ -154,12 +167,12 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
       }
       info.insert(info.end(), gi_info.begin(), gi_info.end());
     }
-    a.wave_info = upload_vec(ws.cand_info, info, "copy candidate wave table to device");
-    a.tiles = upload_vec(ws.cand_tiles, tiles, "copy candidate tile table to device");
+    a.wave_info = upload_vec(ws.cand_info, info, "copy candidate wave table to device", stream);
+    a.tiles = upload_vec(ws.cand_tiles, tiles, "copy candidate tile table to device", stream);
     a.num_waves = max_waves;
     a.info_grp_stride = max_waves * kScoreInfoWords;
     std::vector<int64_t> ids(t.host, t.host + groups * per_target);
-    d_targets = upload_vec(ws.cand_ids, ids, "copy candidates to device");
+    d_targets = upload_vec(ws.cand_ids, ids, "copy candidates to device", stream);
   }
 
   // 4. Score; the batch-row sums over query tokens are taken in the kernel

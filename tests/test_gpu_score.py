@@ -321,3 +321,32 @@ def test_binary_small_dim(gpu, oracle, dim):
     got = h.maxsim_batch(query)
     exp = np.stack([oracle.binary_lut_maxsim(qb, codes, offsets, dim) for qb in query])
     _close(got, exp)
+
+
+def test_score_async_weights_ordered_on_side_stream(gpu):
+    """Back-to-back msim_int4_score_async calls with different reducer weights
+    on a non-blocking stream: each call's weights are uploaded on that stream,
+    after the previous call's kernel, so every output equals the synchronous
+    API's scores for its own weights."""
+    import torch
+
+    from maxsim_amd import _maxsim_hip, synthetic
+    from maxsim_amd._native import check, ptr
+
+    corpus = synthetic.make_corpus(2048, 64, 192, seed=91)
+    query = synthetic.make_queries(corpus, 4)
+    _, h = _int4_handle(corpus.embeddings, corpus.offsets, "token")
+    b, q = query.shape[:2]
+    rng = np.random.default_rng(92)
+    weights = [rng.uniform(0.5, 1.5, size=(b, q)).astype(np.float32) for _ in range(6)]
+    dq = torch.from_numpy(query).cuda()
+    outs = [torch.empty((b, 2048), dtype=torch.float32, device="cuda") for _ in weights]
+    side = torch.cuda.Stream()
+    sptr = _maxsim_hip._stream_ptr(side)
+    torch.cuda.synchronize()
+    for w, out in zip(weights, outs):
+        check(h._lib.msim_int4_score_async(h._h, ptr(dq), b, q, b"weighted_maxsim", ptr(w), 2, b, q, 1.0, 0,
+                                           ptr(out), sptr))
+    side.synchronize()
+    for w, out in zip(weights, outs):
+        np.testing.assert_array_equal(out.cpu().numpy(), h.score_batch(query, "weighted_maxsim", w))
