@@ -567,6 +567,42 @@ class CudaPackedDocs:
         return "mfma_sign_i8"
 
 
+def _binary_free_inputs(query, packed, offsets, dim, query_ndim):
+    """validate_inputs / validate_batch_inputs (cuda_extension.cu:1826-1870):
+    the reference's order of checks and messages."""
+    q, p, o = _f32(query), _u8(packed), _i64(offsets)
+    if q.ndim != query_ndim:
+        raise ValueError("query must have shape [query_tokens, dim]" if query_ndim == 2
+                         else "query must have shape [batch, query_tokens, dim]")
+    if p.ndim != 2:
+        raise ValueError("packed must have shape [num_doc_tokens, dim / 8]")
+    if o.ndim != 1:
+        raise ValueError("offsets must be a 1-D array")
+    dim = int(dim)
+    if dim <= 0 or dim % 8 != 0:
+        raise ValueError("dim must be positive and divisible by 8")
+    if q.shape[-1] != dim or p.shape[1] != dim // 8:
+        raise ValueError("query/packed shapes do not match dim")
+    return q, p, o, dim
+
+
+def maxsim_cuda(query, packed, offsets, dim: int, scale: float = 1.0):
+    """maxsim_cuda(query f32[Q, dim], packed u8[T, dim/8], offsets i64[N+1],
+    dim, scale) -> f32[N] (cuda_extension.cu:3308-3358): binary MaxSim of one
+    fp32 query against host-resident sign-bit documents, uploaded for the
+    call (the reference's _score_binary calls it for CPU-resident documents
+    with device="cuda", _api.py:357-371)."""
+    q, p, o, dim = _binary_free_inputs(query, packed, offsets, dim, 2)
+    return CudaPackedDocs(p, o, dim).maxsim_batch(q[None], scale=float(scale))[0]
+
+
+def maxsim_cuda_batch(query, packed, offsets, dim: int, scale: float = 1.0):
+    """maxsim_cuda_batch(query f32[B, Q, dim], ...) -> f32[B, N]
+    (cuda_extension.cu:3360-3411): maxsim_cuda for a batch of queries."""
+    q, p, o, dim = _binary_free_inputs(query, packed, offsets, dim, 3)
+    return CudaPackedDocs(p, o, dim).maxsim_batch(q, scale=float(scale))
+
+
 def _stream_ptr(stream):
     if stream is None:
         try:

@@ -350,3 +350,22 @@ def test_score_async_weights_ordered_on_side_stream(gpu):
     side.synchronize()
     for w, out in zip(weights, outs):
         np.testing.assert_array_equal(out.cpu().numpy(), h.score_batch(query, "weighted_maxsim", w))
+
+
+def test_maxsim_cuda_free_functions_match_reference_lut(gpu, oracle):
+    """maxsim_cuda / maxsim_cuda_batch (cuda_extension.cu:3308-3412), the
+    handle module's free functions the reference's _score_binary calls for
+    host-resident sign-bit documents (_api.py:357-371): against the oracle
+    LUT (pinned to the reference's compiled maxsim_lut), with a scale, and
+    equal to the resident handle's scores."""
+    from maxsim_amd import _maxsim_hip
+
+    docs, offsets = ragged_fixture(120, 61, lo=1, hi=30)
+    query = np.random.default_rng(62).standard_normal((3, 7, 128)).astype(np.float32)
+    codes, h = _binary_handle(oracle, docs, offsets)
+    one = _maxsim_hip.maxsim_cuda(query[0], codes, offsets, 128, 0.5)
+    _close(one, oracle.binary_lut_maxsim(query[0], codes, offsets, 128, 0.5))
+    batch = _maxsim_hip.maxsim_cuda_batch(query, codes, offsets, 128)
+    _close(batch, np.stack([oracle.binary_lut_maxsim(qb, codes, offsets, 128) for qb in query]))
+    np.testing.assert_array_equal(batch, h.maxsim_batch(query))
+    np.testing.assert_array_equal(_maxsim_hip.maxsim_cuda(query[1], codes, offsets, 128), batch[1])

@@ -272,3 +272,26 @@ def test_bench_refuses_more_than_one_gpu():
                           timeout=120)
     assert proc.returncode == 2
     assert "one GPU" in proc.stderr
+
+
+@pytest.mark.parametrize("args, match", [
+    ((np.zeros((2, 2, 8), np.float32), np.zeros((3, 1), np.uint8), [0, 3], 8), r"query must have shape \[query_tokens, dim\]"),
+    ((np.zeros((2, 8), np.float32), np.zeros(3, np.uint8), [0, 3], 8), r"packed must have shape \[num_doc_tokens, dim / 8\]"),
+    ((np.zeros((2, 8), np.float32), np.zeros((3, 1), np.uint8), [[0, 3]], 8), "offsets must be a 1-D array"),
+    ((np.zeros((2, 8), np.float32), np.zeros((3, 1), np.uint8), [0, 3], 12), "dim must be positive and divisible by 8"),
+    ((np.zeros((2, 16), np.float32), np.zeros((3, 1), np.uint8), [0, 3], 8), "query/packed shapes do not match dim"),
+])
+def test_maxsim_cuda_validation_without_device(args, match):
+    """maxsim_cuda's argument checks in the reference's order and wording
+    (validate_inputs, cuda_extension.cu:1826-1847), before any device work."""
+    from maxsim_amd import _maxsim_hip
+
+    with pytest.raises(ValueError, match=match):
+        _maxsim_hip.maxsim_cuda(*args)
+
+
+def test_maxsim_cuda_batch_requires_3d_query():
+    from maxsim_amd import _maxsim_hip
+
+    with pytest.raises(ValueError, match=r"query must have shape \[batch, query_tokens, dim\]"):
+        _maxsim_hip.maxsim_cuda_batch(np.zeros((2, 8), np.float32), np.zeros((3, 1), np.uint8), [0, 3], 8)
