@@ -38,7 +38,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-SCAN_KERNEL = "int8q_scan_kernel<8, true, true>"  # the scan with its fused top-k tail
+SCAN_KERNEL = "int8q_scan_kernel<8, 1, true>"  # the scan (one-fma epilogue) with its fused top-k tail
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "int8q_scan_config2_traffic.md")
 CALIBRATION_BYTES = 256 << 20  # one plain copy: reads and writes this many bytes
 SCAN_BLOCK = 10  # scan launches between two events
@@ -125,33 +125,63 @@ def read_traffic() -> float | None:
     return None
 
 
+def host_metadata() -> dict:
+    """What the run was: command, host CPU model and core counts, GPU, ROCm."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    meta = {"benchmark_command": " ".join([os.path.basename(sys.executable)] + sys.argv),
+            "cpu_model": model, "nproc": os.cpu_count(), "cpus_allowed": len(os.sched_getaffinity(0))}
+    try:
+        import torch
+
+        meta.update(gpu=torch.cuda.get_device_name(0), hip=torch.version.hip, torch=torch.__version__)
+    except Exception:  # noqa: BLE001 - metadata only
+        pass
+    return meta
+
+
 def cpu_baseline(packed, query, seconds: float):
     """The C oracle (one thread) on a bounded sample of the same workload: whole
     config-2 calls (quantise + scan of every document + top-10), repeated until
-    about `seconds` have passed."""
+    about `seconds` have passed.  The thread is pinned to one core for the
+    measurement (the reference's `taskset -c 0` protocol) and unpinned after."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
 
     orc.build()
-    docs = 0
-    start = time.perf_counter()
-    reps = 0
-    while True:
-        scores = orc.int4_int8q_scores(query, packed.values, packed.doc_offsets, token_scale=packed.token_scale)
-        orc.topk(scores, 10)
-        reps += 1
-        docs += query.shape[0] * (packed.doc_offsets.shape[0] - 1)
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds:
-            break
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[0]
+    os.sched_setaffinity(0, {core})
+    try:
+        docs = 0
+        start = time.perf_counter()
+        reps = 0
+        while True:
+            scores = orc.int4_int8q_scores(query, packed.values, packed.doc_offsets, token_scale=packed.token_scale)
+            orc.topk(scores, 10)
+            reps += 1
+            docs += query.shape[0] * (packed.doc_offsets.shape[0] - 1)
+            elapsed = time.perf_counter() - start
+            if elapsed >= seconds:
+                break
+    finally:
+        os.sched_setaffinity(0, set(allowed))
     return {
         "value": docs / elapsed,
         "unit": "docs scored/s",
         "cores": 1,
         "kind": "port",
+        "pinned_core": core,
         "sample": f"{reps} full config-2 call(s): [{query.shape[0]},{query.shape[1]},128] query x "
                   f"{packed.doc_offsets.shape[0] - 1} docs + top-10, C oracle (oracle/maxsim_oracle.c), "
-                  f"1 thread, {elapsed:.1f} s",
+                  f"1 thread pinned to core {core}, {elapsed:.1f} s",
         "ms_per_call": 1e3 * elapsed / reps,
     }
 
@@ -280,13 +310,26 @@ def bench_config2(args):
     scan_avg_s = float(scan_ms.mean()) * 1e-3
     achieved = nbytes["total"] / scan_avg_s / 1e9
 
+
     # ---- MALL-cold: rotate over corpus copies whose total exceeds the 256 MB cache.
     cold = None
+    cold_scan_ms = None
     if args.cold_copies > 0:
         copies = [handle] + [int4_to_device(packed).data for _ in range(args.cold_copies - 1)]
         for c in copies:
             step(c)
         torch.cuda.synchronize()
+        # the scan kernel alone, each launch on the next copy (its query quantised beforehand)
+        for c in copies:
+            check(lib.msim_int4_quantize_int8q_async(c._h, ptr(query), batch, qtok, sptr))
+        rot = [0]
+
+        def cold_launch():
+            c = copies[rot[0] % len(copies)]
+            rot[0] += 1
+            check(lib.msim_int4_topk_quantized_async(c._h, batch, qtok, k, ptr(top_s), ptr(top_i), sptr))
+
+        cold_scan_ms = block_times(cold_launch)
         cev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
         t1 = time.perf_counter()
         for i in range(args.steps):
@@ -313,15 +356,29 @@ def bench_config2(args):
         torch.cuda.synchronize()
         del src, dst
 
-    # ---- synchronous host API (numpy in, numpy out), the reference's protocol.
-    for _ in range(5):
-        handle.topk_batch_int8q(query_np, k)
-    api = []
-    for _ in range(60):
-        a = time.perf_counter()
-        handle.topk_batch_int8q(query_np, k)
-        api.append(1e3 * (time.perf_counter() - a))
-    api = np.array(api)
+    # ---- synchronous host API (numpy in, numpy out) and the end-to-end
+    # Reranker.search, the reference's protocol (run_cuda_step1.py:690-736):
+    # 3 runs x 20 calls after 5 warm-ups, p50 / p95.
+    def host_timed(call):
+        for _ in range(5):
+            call()
+        out = []
+        for _ in range(3 * 20):
+            a = time.perf_counter()
+            call()
+            out.append(1e3 * (time.perf_counter() - a))
+        return np.array(out)
+
+    api = host_timed(lambda: handle.topk_batch_int8q(query_np, k))
+    import maxsim_amd
+
+    ids = [f"doc{i}" for i in range(num_docs)]
+    index = maxsim_amd.Index.from_embeddings(ids, corpus.embeddings, corpus.offsets, mode="int4_per_token")
+    reranker = maxsim_amd.Reranker(index, device="cuda", int4_query="int8")
+    res = reranker.search(query_np, k=k)
+    assert [[r.doc_id for r in row] for row in res] == [[ids[i] for i in row] for row in ref_ids], \
+        "Reranker.search differs from the device top-k"
+    search = host_timed(lambda: reranker.search(query_np, k=k))
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(packed, query_np, args.cpu_seconds)
     cpu_all = None if args.no_cpu_baseline else cpu_baseline_threads(packed, query_np, args.cpu_seconds / 3)
@@ -367,13 +424,26 @@ def bench_config2(args):
             "scoring_only_ms_avg": float(score_ms.mean()),
             "scoring_only_frac": (nbytes["total"] - 4 * batch * num_docs - 12 * batch * k)
                                  / (float(score_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "cold_kernel_ms_avg": None if cold_scan_ms is None else float(cold_scan_ms.mean()),
+            "cold_frac": None if cold_scan_ms is None
+                         else nbytes["total"] / (float(cold_scan_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "traffic_source": "profiles/int8q_scan_config2_traffic.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
+                              "runs of this script, calibrated by a plain copy)",
             "note": "scan launches (with the fused top-10) back to back, averaged over blocks of %d; the "
-                    "35.7 MB corpus stays in the 256 MB MALL between launches" % SCAN_BLOCK,
+                    "35.7 MB corpus stays in the 256 MB MALL between launches (cold_*: each launch on the "
+                    "next of %d corpus copies, %.0f MB in all)" % (SCAN_BLOCK, max(1, args.cold_copies),
+                                                                  max(1, args.cold_copies) * nbytes["corpus"] / 1e6),
         },
         "mall_cold": cold,
         "api_sync_ms": {"p50": float(np.percentile(api, 50)), "p95": float(np.percentile(api, 95))},
+        "reranker_search_ms": {"p50": float(np.percentile(search, 50)), "p95": float(np.percentile(search, 95)),
+                               "calls": int(search.shape[0]),
+                               "route": "maxsim_amd.Reranker(index, device='cuda', int4_query='int8').search("
+                                        "query [4,32,128] numpy, k=10): H2D query, quantise + fused scan, D2H, "
+                                        "SearchResult lists"},
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,
+        "metadata": host_metadata(),
     }
     print(json.dumps(result), flush=True)
 
@@ -457,6 +527,22 @@ def bench_config3(args):
         assert np.array_equal(scores.cpu().numpy(), ref), f"{red}: device-resident scores differ from the host API"
         wall, ev = _timed(step, args.steps, args.warmup, stream)
         per[red] = {"ms_per_step": wall, "p50_ms": float(np.percentile(ev, 50)), "docs_per_s": b * n / (wall * 1e-3)}
+    # weighted MaxSim with new weights every step (two arrays alternating, so
+    # the handle's unchanged-weights check never skips the upload)
+    other = np.ascontiguousarray(weights[::-1])
+    flip = [0]
+
+    def fresh_step():
+        w = weights if flip[0] % 2 == 0 else other
+        flip[0] += 1
+        check(lib.msim_int4_score_async(h._h, ptr(dq), b, q, b"weighted_maxsim", ptr(w), 2, b, q, 1.0, 0,
+                                        ptr(scores), sptr))
+        check(lib.msim_topk_async(ptr(scores), b, n, n, args.k, ptr(ts), ptr(ti), sptr))
+
+    wall, ev = _timed(fresh_step, args.steps, args.warmup, stream)
+    fresh = {"ms_per_step": wall, "p50_ms": float(np.percentile(ev, 50)), "docs_per_s": b * n / (wall * 1e-3),
+             "note": "weighted_maxsim with different weights every step (a host-to-device copy of the weights "
+                     "on the stream each step)"}
     ms = float(np.mean([v["ms_per_step"] for v in per.values()]))
     ops = 2.0 * b * q * t * 128  # multiply-adds x 2 of the fp32 contraction
     roof = {"kernel": "score_kernel (3 int8 limbs)", "bound": "mfma", "unit": "TOP/s",
@@ -480,7 +566,7 @@ def bench_config3(args):
                    "docs scored/s", args, ms, float(np.mean([v["p50_ms"] for v in per.values()])), None, "f32",
                    "BASELINE config 3: config-2 corpus, fp32 query [4,32,128], reducers maxsim / weighted (U[0.5,1.5]) "
                    "/ topk2 / topk4 / smoothsim (tau 0.7), top-10",
-                   {"per_reducer": per, "roofline": roof, "cpu_baseline": cpu})
+                   {"per_reducer": per, "weighted_maxsim_fresh_weights": fresh, "roofline": roof, "cpu_baseline": cpu})
 
 
 def bench_config4(args):
