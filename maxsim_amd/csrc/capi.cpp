@@ -243,6 +243,7 @@ void build_wave_info(msim_int4_docs* h, int64_t waves) {
   std::vector<uint64_t> tiles;
   build_scan_tables(h->host_offsets.data(), h->num_docs, waves, g_scan_partition == 1, info, tiles, h->tile_stride,
                     h->num_scan_waves);
+  h->block_pos_off = (int64_t)info.size() - (h->num_scan_waves / kScanWavesPerGroup + 1);
   h->wave_info.ensure(sizeof(int64_t) * std::max<size_t>(1, info.size()), "hipMalloc scan wave table");
   if (!info.empty())
     check_hip(hipMemcpy(h->wave_info.ptr, info.data(), sizeof(int64_t) * info.size(), hipMemcpyHostToDevice),
@@ -286,6 +287,7 @@ void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a
   a.scale = h->scale;
   a.score_stride = h->num_docs;
   a.num_docs = h->num_docs;
+  a.block_pos = h->wave_info.as<int64_t>() + h->block_pos_off;
 }
 
 }  // namespace msim
@@ -293,12 +295,16 @@ void scan_corpus_args(const msim_int4_docs* h, int64_t query_tokens, ScanArgs& a
 namespace {
 
 // The scan selects the top-k itself (last-workgroup tail) when every pass's
-// batch rows and the corpus fit the tail's limits.
-bool scan_fuses_topk(const msim_int4_docs* h, int64_t batch, int64_t query_tokens, int64_t k) {
+// batch rows, the corpus and the scan's workgroup count fit the tail's
+// limits (builds the scan tables if needed).
+bool scan_fuses_topk(msim_int4_docs* h, int64_t batch, int64_t query_tokens, int64_t k) {
   if (g_fused_topk == 0 || k <= 0 || query_tokens == 0 || query_tokens > 128 || h->num_docs == 0) return false;
   const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
-  return k <= msim::kScanTailMaxK && h->num_docs >= msim::kScanTailMinDocs && h->num_docs <= msim::kScanTailMaxDocs &&
-         std::min(per_pass, batch) <= msim::kScanTailMaxRows;
+  if (!(k <= msim::kScanTailMaxK && h->num_docs >= msim::kScanTailMinDocs && h->num_docs <= msim::kScanTailMaxDocs &&
+        std::min(per_pass, batch) <= msim::kScanTailMaxRows))
+    return false;
+  build_wave_info(h, scan_waves(h));
+  return h->num_scan_waves <= (int64_t)kScanWavesPerGroup * kScanTailBlocks;
 }
 
 // Scores of the quantised query against every document into d_scores [B, N];
@@ -317,19 +323,30 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
   ScanArgs a{};
   scan_corpus_args(h, query_tokens, a);
   if (k > 0) {
-    // A fill kernel, not a memset, so that a captured call records no memset
-    // node; it runs once per allocation (the selecting workgroup resets the
-    // ticket).
-    if (h->ticket.ptr == nullptr) {
-      h->ticket.ensure(256, "hipMalloc scan ticket");
-      check_hip(launch_fill_f32(h->ticket.as<float>(), 1, 0.0f, stream), "zero scan ticket");
+    // Fill kernels, not memsets, so that a captured call records no memset
+    // node; they run once per allocation: the launch counter starts at 0 and
+    // the key and block-maximum rows hold no tag of a later launch.
+    if (h->tail_epoch.ptr == nullptr) {
+      h->tail_epoch.ensure(256, "hipMalloc scan launch counter");
+      check_hip(launch_fill_f32(h->tail_epoch.as<float>(), 1, 0.0f, stream), "zero scan launch counter");
     }
-    h->tail_scores.ensure(sizeof(float) * (size_t)(batch * kScanTailRow), "hipMalloc scan tail rows");
-    d_scores = h->tail_scores.as<float>();
-    a.score_stride = kScanTailRow;
+    const int64_t rows = std::min(batch, std::max<int64_t>(1, kScanPassRows / query_tokens));
+    const size_t key_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailRow);
+    const size_t bmax_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailBlocks);
+    if (h->tail_keys.cap < key_bytes) {
+      h->tail_keys.ensure(key_bytes, "hipMalloc scan tail key rows");
+      check_hip(launch_fill_f32(h->tail_keys.as<float>(), (int64_t)(key_bytes / 4), 0.0f, stream), "zero scan tail key rows");
+    }
+    if (h->tail_bmax.cap < bmax_bytes) {
+      h->tail_bmax.ensure(bmax_bytes, "hipMalloc scan tail block maxima");
+      check_hip(launch_fill_f32(h->tail_bmax.as<float>(), (int64_t)(bmax_bytes / 4), 0.0f, stream),
+                "zero scan tail block maxima");
+    }
+    a.tail_keys = h->tail_keys.as<uint64_t>();
+    a.tail_bmax = h->tail_bmax.as<uint64_t>();
     a.topk_k = (int32_t)k;
     a.tail_cap = g_fused_topk == 2 ? 0 : INT32_MAX;
-    a.ticket = h->ticket.as<uint32_t>();
+    a.epoch = h->tail_epoch.as<uint32_t>();
   }
   const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
   for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
@@ -337,7 +354,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     a.qpack = h->qpack.as<int8_t>() + (b0 / per_pass) * scan_qpack_bytes(per_pass * query_tokens, per_pass * query_tokens);
     a.qscale = h->qscale.as<float>() + b0 * query_tokens;
     a.batch = (int32_t)nb;
-    a.scores = d_scores + b0 * a.score_stride;
+    a.scores = k > 0 ? nullptr : d_scores + b0 * a.score_stride;
     if (k > 0) {
       a.top_scores = d_top_s + b0 * k;
       a.top_ids = d_top_i + b0 * k;

@@ -104,6 +104,7 @@ struct msim_int4_docs {
   int partition_mode = 0;         // msim_set_scan_partition mode it was built with
   int64_t num_scan_waves = 0;     // rows of wave_info
   int64_t tile_stride = 0;        // tile-table entries per wave
+  int64_t block_pos_off = 0;      // index of the workgroup start positions in wave_info
   msim::DeviceBuffer wave_info, tile_table;
   msim::DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales16;
   // Generalized path: codes padded to 64 bytes per token when dim < 128,
@@ -111,9 +112,9 @@ struct msim_int4_docs {
   msim::DeviceBuffer codes128, residual128, ones16;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
-  // Scan with fused top-k: workgroup ticket (zero between launches) and score
-  // rows of kScanTailRow floats.
-  msim::DeviceBuffer ticket, tail_scores;
+  // Scan with fused top-k: launch counter, key rows of kScanTailRow tagged
+  // 64-bit keys and block-maximum rows of kScanTailBlocks tagged entries.
+  msim::DeviceBuffer tail_epoch, tail_keys, tail_bmax;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
@@ -122,7 +123,7 @@ struct msim_int4_docs {
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap + top_indices.cap +
-           rowmax.cap + wave_info.cap + tile_table.cap + ticket.cap + tail_scores.cap + ws.bytes();
+           rowmax.cap + wave_info.cap + tile_table.cap + tail_epoch.cap + tail_keys.cap + tail_bmax.cap + ws.bytes();
   }
 };
 

@@ -36,6 +36,12 @@ __device__ __forceinline__ uint64_t load_b64(__amdgpu_buffer_rsrc_t r, int byte_
   return ((uint64_t)v.y << 32) | v.x;
 }
 
+__device__ __forceinline__ uint64_t load_b64_coherent(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_offset, 0, kCoherentLoadPolicy);
+  return ((uint64_t)v.y << 32) | v.x;
+}
+
 __device__ __forceinline__ unsigned load_b32(__amdgpu_buffer_rsrc_t r, int byte_offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 0);
 }
@@ -119,6 +125,14 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Workgroup barrier that orders LDS only: global stores still in flight are
+// not waited for (__syncthreads would wait for them).
+__device__ __forceinline__ void group_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Value of lane 4 * (l / 4) + I in every lane l (DPP quad permute).

@@ -31,9 +31,10 @@
 //    in registers (permlane swaps scatter batch row b to lane group b, DPP
 //    moves order the pairwise sum), otherwise through LDS;
 //  * fused selection (ScanArgs::topk_k > 0): scores are stored write-through
-//    and every workgroup takes a ticket once its stores have completed; the
-//    last one selects each batch row's top-k (topk_block.hpp, tail form),
-//    one wave per row, in its own LDS.
+//    as tagged keys, each workgroup's largest key per batch row likewise;
+//    workgroup 0, once its own documents are done, waits until what it reads
+//    carries the launch's tag and selects each batch row's top-k
+//    (topk_block.hpp, tail form), one wave per row, in its own LDS.
 #include "common.hpp"
 #include "internal.hpp"
 #include "topk_block.hpp"
@@ -44,7 +45,10 @@ constexpr int kScanThreads = 256;
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kPrefetch = kScanPrefetch;  // tiles in flight per wave
 static_assert(kPrefetch >= 2, "ring of at least two tiles");
-static_assert(kScanTailRow == kTailRow && kScanTailMaxDocs <= kTailRow, "fused selection rows");
+static_assert(kScanTailBlocks == kTailBlocks && kScanTailMaxDocs <= kScanTailRow && kScanTailMaxDocs <= kTailMaxDocs,
+              "fused selection sizes");
+static_assert(kScanTailMaxRows <= kScanThreads, "one thread per batch row writes the block maxima");
+static_assert(kPrefetch * kWave * 16 >= kTailLdsBytes, "a wave's tile ring holds the selection's candidates");
 static_assert(kScanTailMaxK <= kWave, "fused selection k");
 
 // Maximum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
@@ -80,21 +84,13 @@ __device__ __forceinline__ double dpp_f64(double v) {
   return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
 }
 
-// A score store; write-through (agent-scope atomic) when the launch selects
-// its top-k from scores written by other workgroups.
-__device__ __forceinline__ void put_score(float* p, float v, bool coherent) {
-  if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *p = v;
-}
-
-// out[b * stride] = f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale), b < batch.
+// emit(b, f32(pairwise_f64(max[b,q] * sigma[b,q]) * scale)) for b < batch.
 // rows = batch * query_tokens <= 128, so query_tokens < 8 means batch <= 128
 // (lanes b and b + 64) and query_tokens >= 8 means batch <= 16 (two rounds of
-// eight lanes per batch row).  Each path issues at most two global stores.
+// eight lanes per batch row).  Each path emits at most twice per lane.
+template <class Emit>
 static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, const float* qs, int batch,
-                                                       int query_tokens, double scale,
-                                                       float* __restrict__ out, int64_t stride,
-                                                       bool coherent) {
+                                                       int query_tokens, double scale, Emit emit) {
   const int lane = lane_id();
   auto prod = [&](int r) -> double { return (double)rowmax[r] * (double)qs[r]; };
   if (query_tokens < 8) {
@@ -104,7 +100,7 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
       double res = 0.0;
       if (b < batch) {
         for (int q = 0; q < query_tokens; ++q) res = __dadd_rn(res, prod(b * query_tokens + q));
-        put_score(out + (int64_t)b * stride, (float)(res * scale), coherent);
+        emit(b, (float)(res * scale));
       }
     }
     return;
@@ -126,7 +122,7 @@ static __device__ __forceinline__ void scan_finish_doc(const float* rowmax, cons
     if (k == 0) r = __dadd_rn(r, o);
     if (k == 0 && valid) {
       for (int i = body; i < query_tokens; ++i) r = __dadd_rn(r, prod(base + i));
-      put_score(out + (int64_t)b * stride, (float)(r * scale), coherent);
+      emit(b, (float)(r * scale));
     }
   }
 }
@@ -177,6 +173,25 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   constexpr bool fused = kTail;  // p.topk_k > 0 exactly when kTail
   float* rowmax = s_rowmax[wave];
   float* qs = s_qscale[wave];
+  // Fused selection: documents take positions pos0, pos0 + 1, ... (the
+  // wave's empty documents, then the others in tile order); per batch row
+  // the largest score key of the wave's documents.
+  __shared__ uint32_t s_bmax[kScanWaves][kScanTailMaxRows];
+  const int pos0 = (int)info[5];
+  int nfin = 0;
+  uint32_t tag = 0;  // the launch's tag (fused), read below
+  if (fused && lane < kScanTailMaxRows) s_bmax[wave][lane] = 0u;
+  // Score v of document doc for batch row b, at position pos.
+  auto emit = [&](int b, int64_t doc, int pos, float v) {
+    if constexpr (fused) {
+      const uint64_t key = tail_full_key(v, (uint32_t)doc, tag);
+      __hip_atomic_store(p.tail_keys + (int64_t)b * kScanTailRow + pos, key, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      atomicMax(&s_bmax[wave][b], (uint32_t)(key >> 32));
+    } else {
+      scores[(int64_t)b * p.score_stride + doc] = v;
+    }
+  };
 
   // Global loads, all with an LDS destination (untracked by the compiler,
   // waited for explicitly), in this order: the workgroup's query tiles (each
@@ -194,6 +209,9 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     const uint32_t qs_lds = wave_uniform((int)lds_address(qs));
     lds_load_b32(rq, 4u * (uint32_t)lane, qs_lds);
     lds_load_b32(rq, 4u * (uint32_t)(lane + kWave), qs_lds + 4 * kWave);
+    // Fused: the launch counter into lane 0's word of the row-maxima buffer
+    // (the other lanes read past the 4-byte range: 0).
+    if (fused) lds_load_b32(make_rsrc_words(p.epoch, 4u), 4u * (uint32_t)lane, wave_uniform((int)lds_address(rowmax)));
   }
 
   // Bounds-checked descriptors over the wave's tokens (rows past the wave
@@ -224,6 +242,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // loads are outstanding; the barrier publishes all four quarters.
   vm_wait_lds<kPrefetch * kOps>();
   __builtin_amdgcn_s_barrier();
+  if (fused) tag = (uint32_t)wave_uniform((int)__float_as_uint(rowmax[0])) + 1u;
   // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g; half j
   // of tile h is the linear 1 KiB run 2j + h (no bank conflicts).
   v4i blo[NT], bhi[NT];
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       r = __dadd_rn(r, dpp_f64<0xB1>(r));   // quad_perm [1,0,3,2]
       r = __dadd_rn(r, dpp_f64<0x4E>(r));   // quad_perm [2,3,0,1]
       r = __dadd_rn(r, dpp_f64<0x141>(r));  // row_half_mirror
-      if (c == 0 && g < p.batch) put_score(scores + d0 + local + (int64_t)g * p.score_stride, (float)(r * p.scale), fused);
+      if (c == 0 && g < p.batch) emit(g, d0 + local, pos0 + nempty + nfin, (float)(r * p.scale));
     } else {
 #pragma unroll
       for (int j = 0; j < NT; ++j) mf[j] = unfold(max_over_groups(mf[j]));
@@ -374,7 +393,8 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
         for (int j = 0; j < NT; ++j) rowmax[16 * j + c] = mf[j];
       }
       wave_sync_lds();
-      scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale, scores + d0 + local, p.score_stride, fused);
+      scan_finish_doc(rowmax, qs, p.batch, p.query_tokens, p.scale,
+                      [&](int b, float v) { emit(b, d0 + local, pos0 + nempty + nfin, v); });
       wave_sync_lds();
     }
 #pragma unroll
@@ -382,6 +402,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       m[j] = kNegInf;
       mi[j] = INT32_MIN;
     }
+    ++nfin;
   };
 
   // Software pipeline over the wave's tiles.  Step i: the MFMAs of tile
@@ -447,36 +468,42 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       last(acc_a);
     }
   }
-  // No LDS-destination load may still be in flight when the wave ends.
-  vm_wait_lds<0>();
+  // No LDS-destination load may still be in flight when the wave ends (a
+  // fused launch waits later: that wait also covers its key stores).
+  if (!fused) vm_wait_lds<0>();
 
   // Empty documents score 0 (the wave's entries of the empty-document list).
   for (int e = lane; e < nempty; e += kWave) {
     const int64_t doc = wave_info_ptr[p.num_waves * kWaveInfoWords + e0 + e];
-    for (int b = 0; b < p.batch; ++b) put_score(scores + (int64_t)b * p.score_stride + doc, 0.0f, fused);
+    for (int b = 0; b < p.batch; ++b) emit(b, doc, pos0 + e, 0.0f);
   }
   if constexpr (!fused) return;
 
-  // Fused selection.  Each wave waits until its write-through score stores
-  // have completed, then one thread takes a ticket; the workgroup holding the
-  // last ticket has every score of the launch visible to agent-scope loads.
-  __shared__ uint32_t s_last;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t ticket = __hip_atomic_fetch_add(p.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = ticket == gridDim.x - 1 ? 1u : 0u;
+  // Fused selection.  The workgroup's block maxima (one thread per batch
+  // row, after an LDS-only barrier: the key stores stay in flight), tagged.
+  // Every workgroup but 0 is then done; workgroup 0 selects (each of its
+  // waves once its own tile ring has drained).
+  int bs[kTailBlocksPerLane], blen[kTailBlocksPerLane];
+  if (blockIdx.x == 0) tail_block_ranges(p.block_pos, (int)gridDim.x, bs, blen);
+  group_sync_lds();
+  if ((int)threadIdx.x < p.batch) {
+    uint32_t bm = 0;
+#pragma unroll
+    for (int w = 0; w < kScanWaves; ++w) bm = max(bm, s_bmax[w][threadIdx.x]);
+    __hip_atomic_store(p.tail_bmax + (int64_t)threadIdx.x * kScanTailBlocks + blockIdx.x, ((uint64_t)bm << 32) | tag,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  if (s_last == 0) return;
-  // Wave w selects batch rows w, w + 4, ...; its tile ring holds the candidates.
-  uint64_t* cand = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
-  constexpr int kCap = (int)(sizeof(s_codes[0]) / sizeof(uint64_t)) - kWave;  // and a spare entry per lane
+  vm_wait_lds<0>();
+  if (blockIdx.x != 0) return;
+  // Wave w selects batch rows w, w + 4, ... in its tile ring's LDS.
+  uint64_t* lds = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
   for (int b = wave; b < p.batch; b += kScanWaves)
-    tail_topk(scores + (int64_t)b * p.score_stride, (int)p.num_docs, p.topk_k, cand, min(kCap, p.tail_cap),
-              p.top_scores + (int64_t)b * p.topk_k,
+    tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_bmax + (int64_t)b * kScanTailBlocks, (int)gridDim.x,
+              (int)p.num_docs, p.topk_k, p.tail_cap, tag, lds, bs, blen, p.top_scores + (int64_t)b * p.topk_k,
               p.top_ids + (int64_t)b * p.topk_k);
-  if (threadIdx.x == 0) __hip_atomic_store(p.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Every workgroup read the counter at its start, before its block maxima
+  // that the selection waited for: the next launch's tag can be published.
+  if (threadIdx.x == 0) __hip_atomic_store(p.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int EPI, bool kTail>
@@ -513,9 +540,10 @@ hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t str
   if ((epilogue == kScanEpiIntMax) != (args.token_scale16 == nullptr)) return hipErrorInvalidValue;
   if (args.topk_k > 0 &&
       (args.topk_k > kScanTailMaxK || args.topk_k > args.num_docs || args.num_docs > kScanTailMaxDocs ||
-       args.num_docs < kScanTailMinDocs || args.score_stride != kTailRow || args.batch > kScanTailMaxRows ||
-       args.ticket == nullptr ||
-       args.top_scores == nullptr || args.top_ids == nullptr))
+       args.num_docs < kScanTailMinDocs || args.batch > kScanTailMaxRows ||
+       args.num_waves > (int64_t)kScanWaves * kScanTailBlocks || args.epoch == nullptr ||
+       args.top_scores == nullptr || args.top_ids == nullptr || args.tail_keys == nullptr ||
+       args.tail_bmax == nullptr || args.block_pos == nullptr))
     return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;

@@ -50,7 +50,9 @@ hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int
 //   [1] ndocs       non-empty documents of the wave
 //   [2] T0, [3] T1  token range the wave's tiles lie in, (T1 - T0) * 64 < 2^31
 //   [4] ntiles      16-token tiles of the wave: sum over documents of ceil(len / 16)
-//   [5] tab0        index of the wave's first entry in the tile table
+//   [5] pos0        first position of the wave's documents in the fused
+//                   selection's order (wave order: each wave's empty documents,
+//                   then its other documents in tile order)
 //   [6] nempty      empty documents the wave writes 0 for
 //   [7] e0          their first entry in the empty-document list, which
 //                   follows the num_waves rows in the same buffer
@@ -85,25 +87,35 @@ struct ScanArgs {
   int32_t batch;                // batch rows of this pass (batch * query_tokens <= 128)
   int32_t query_tokens;
   double scale;                 // tensor scale (1.0 for per-token corpora)
-  float* scores;                // [batch, score_stride]
+  float* scores;                // [batch, score_stride] (not used by a fused launch)
   int64_t score_stride;
-  // Fused selection (topk_k > 0): scores are stored write-through into rows
-  // of score_stride = kScanTailRow floats (kScanTailMinDocs <= num_docs <=
-  // kScanTailMaxDocs; columns num_docs and up are ignored), and the last
-  // workgroup to take a ticket selects the top-k of every batch row into
-  // top_scores / top_ids [batch, topk_k], then resets *ticket to 0.
+  // Fused selection (topk_k > 0, kScanTailMinDocs <= num_docs <=
+  // kScanTailMaxDocs, num_waves <= 4 * kScanTailBlocks): the launch's tag is
+  // *epoch + 1; every document's score goes write-through, as a tagged 64-bit
+  // selection key (tail_full_key), to its wave-order position of tail_keys
+  // [batch, kScanTailRow]; every workgroup writes the largest 32-bit score key
+  // of its documents per batch row, above the tag, to tail_bmax [batch,
+  // kScanTailBlocks]; workgroup 0 waits until its reads carry the tag, selects
+  // the top-k of every batch row into top_scores / top_ids [batch, topk_k] and
+  // stores the tag to *epoch.  tail_keys and tail_bmax hold no entry with a
+  // later launch's tag (zero them when allocated).  block_pos [num_waves / 4 +
+  // 1] holds each workgroup's first position (then num_docs).
   int32_t topk_k;
-  int32_t tail_cap;             // candidate slots per wave at most (0 forces the k-round path)
+  int32_t tail_cap;             // 0 forces the selection's k-round path
   int64_t num_docs;
-  uint32_t* ticket;             // zero before the launch
+  uint32_t* epoch;
   float* top_scores;
   int64_t* top_ids;
+  uint64_t* tail_keys;
+  uint64_t* tail_bmax;
+  const int64_t* block_pos;
 };
 constexpr int kScanTailMaxK = 32;
 constexpr int64_t kScanTailMaxDocs = 4096;
 constexpr int64_t kScanTailMinDocs = 256;  // every lane of the selecting wave holds a score
-constexpr int64_t kScanTailRow = 4096;  // floats per score row of the fused selection
+constexpr int64_t kScanTailRow = 4096;  // key positions per batch row of the fused selection
 constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
+constexpr int kScanTailBlocks = 512;  // workgroups of a fused launch at most
 // Epilogue forms of the scan (the token scales decide which is exact):
 //  * kScanEpiIntMax: tensor-scale corpora (token_scale16 == nullptr): integer
 //    maximum of the dots, scaled at the document end;
@@ -123,7 +135,9 @@ inline int64_t scan_pass_rows(int64_t query_tokens) {
 // Builds the wave table and tile table for `waves` requested waves (the
 // result may hold more rows: ranges are split at kScanMaxDocsPerWave
 // documents and 2^25 tokens, and padded to whole workgroups).  Each wave's
-// tile entries start at wave * tile_stride.
+// tile entries start at wave * tile_stride.  wave_info ends with the
+// empty-document list and then the num_waves / 4 + 1 workgroup start
+// positions (block_pos of ScanArgs).
 // `contiguous` forces contiguous document ranges (otherwise used only for
 // corpora beyond 2^25 tokens or 2^24 documents).
 void build_scan_tables(const int64_t* offsets, int64_t num_docs, int64_t waves, bool contiguous,

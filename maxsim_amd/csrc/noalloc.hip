@@ -1,17 +1,19 @@
 // noalloc.hip -- msim_int4_topk_int8q_noalloc: the int8-query search of
 // msim_int4_topk_int8q_async with its scratch memory (quantised query, score
-// rows, the fused selection's ticket) in one fixed device array instead of
-// handle workspaces, so a call allocates nothing.  For callers that cannot
-// allocate device memory (code under HIP graph capture, tight serving loops).
+// rows of an unfused call, the fused selection's key rows, block maxima and
+// launch counter) in one fixed device array instead of handle workspaces, so
+// a call allocates nothing.  For callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops).
 //
 // The array `scratch` is a file-scope __device__ object: every GPU the
 // library runs on holds its own copy, at its own address, until the process
-// ends.  Host code never names it after set-up: the first call on a device
-// looks its address up with hipGetSymbolAddress (with that device current)
-// and keeps it per device.  Every call on a GPU shares that GPU's array and
-// leaves its contents behind; calls that overlap on one GPU (different
-// streams, or different host threads) race on it.  The ticket is zeroed at
-// set-up and the selecting workgroup resets it at the end of every launch.
+// ends, zero-initialised when the code object loads.  Host code never names
+// it after set-up: the first call on a device looks its address up with
+// hipGetSymbolAddress (with that device current) and keeps it per device.
+// Every call on a GPU shares that GPU's array and leaves its contents
+// behind; calls that overlap on one GPU (different streams, or different
+// host threads) race on it.  The launch counter only grows, so entries left
+// by earlier calls (of any handle) carry older tags than the current launch.
 #include <mutex>
 
 #include "capi_handles.hpp"
@@ -25,10 +27,13 @@ constexpr int64_t kNoallocScoreFloats = kScanTailMaxRows * kScanTailRow;  // 32,
 constexpr size_t kQpackOff = 0;
 constexpr size_t kQscaleOff = kQpackOff + kNoallocQueryRows * 128;
 constexpr size_t kQbiasOff = kQscaleOff + kNoallocQueryRows * 4;
-constexpr size_t kScoresOff = kQbiasOff + kNoallocQueryRows * 4;
-constexpr size_t kTicketOff = kScoresOff + kNoallocScoreFloats * 4;
-constexpr size_t kScratchBytes = kTicketOff + 256;  // 166,144 bytes
-static_assert(kScoresOff % 256 == 0 && kTicketOff % 256 == 0, "aligned scratch regions");
+constexpr size_t kScoresOff = kQbiasOff + kNoallocQueryRows * 4;  // score rows of an unfused call
+constexpr size_t kKeysOff = kScoresOff + kNoallocScoreFloats * 4;  // fused: key rows
+constexpr size_t kBmaxOff = kKeysOff + kScanTailMaxRows * kScanTailRow * 8;  // fused: block maxima
+constexpr size_t kEpochOff = kBmaxOff + kScanTailMaxRows * kScanTailBlocks * 8;  // fused: launch counter
+constexpr size_t kScratchBytes = kEpochOff + 256;  // 461,056 bytes
+static_assert(kScoresOff % 256 == 0 && kKeysOff % 256 == 0 && kBmaxOff % 256 == 0 && kEpochOff % 256 == 0,
+              "aligned scratch regions");
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -36,18 +41,16 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 unsigned char* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of this device's `scratch`, looked up (and its ticket
-// zeroed on `stream`) at the first call on the device.
-unsigned char* scratch_on(int device, hipStream_t stream) {
+// Device address of this device's `scratch`, looked up at the first call on
+// the device.
+unsigned char* scratch_on(int device) {
   if (device < 0 || device >= kMaxDevices) throw RuntimeError("device ordinal out of range for the scratch table");
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[device] == nullptr) {
     void* ptr = nullptr;
     check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
     if (ptr == nullptr) throw RuntimeError("hipGetSymbolAddress(scratch) returned no address");
-    auto* base = static_cast<unsigned char*>(ptr);
-    check_hip(launch_fill_f32(reinterpret_cast<float*>(base + kTicketOff), 1, 0.0f, stream), "zero scratch ticket");
-    g_scratch_ptr[device] = base;
+    g_scratch_ptr[device] = static_cast<unsigned char*>(ptr);
   }
   return g_scratch_ptr[device];
 }
@@ -72,8 +75,8 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
     if (k > kScanTailMaxK) throw InvalidArgument("msim_int4_topk_int8q_noalloc takes k <= 32");
     const int64_t n = h->num_docs;
     const int mode = msim_get_fused_topk();
-    const bool fused =
-        mode != 0 && n >= kScanTailMinDocs && n <= kScanTailMaxDocs && batch <= kScanTailMaxRows;
+    const bool fused = mode != 0 && n >= kScanTailMinDocs && n <= kScanTailMaxDocs && batch <= kScanTailMaxRows &&
+                       h->num_scan_waves <= (int64_t)kScanWavesPerGroup * kScanTailBlocks;
     if (!fused && batch * n > kNoallocScoreFloats)
       throw InvalidArgument(
           "msim_int4_topk_int8q_noalloc holds batch * num_docs <= 32768 scores unless the scan selects the top-k "
@@ -84,7 +87,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
           "msim_int4_topk_int8q_async call to rebuild them");
     check_hip(hipSetDevice(h->device), "hipSetDevice");
     const hipStream_t s = as_stream(stream);
-    unsigned char* base = scratch_on(h->device, s);
+    unsigned char* base = scratch_on(h->device);
     auto* qpack = reinterpret_cast<int8_t*>(base + kQpackOff);
     auto* qscale = reinterpret_cast<float*>(base + kQscaleOff);
     auto* qbias = reinterpret_cast<int32_t*>(base + kQbiasOff);
@@ -97,15 +100,16 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
     a.qpack = qpack;
     a.qscale = qscale;
     a.batch = (int32_t)batch;
-    a.scores = scores;
     if (fused) {
-      a.score_stride = kScanTailRow;
+      a.tail_keys = reinterpret_cast<uint64_t*>(base + kKeysOff);
+      a.tail_bmax = reinterpret_cast<uint64_t*>(base + kBmaxOff);
       a.topk_k = (int32_t)k;
       a.tail_cap = mode == 2 ? 0 : INT32_MAX;
-      a.ticket = reinterpret_cast<uint32_t*>(base + kTicketOff);
+      a.epoch = reinterpret_cast<uint32_t*>(base + kEpochOff);
       a.top_scores = d_scores;
       a.top_ids = d_indices;
     }
+    if (!fused) a.scores = scores;
     check_hip(launch_int8q_scan(a, scan_epilogue(h), s), "launch int8q scan kernel");
     if (!fused)
       check_hip(launch_topk(scores, batch, n, n, k, nullptr, d_scores, d_indices, s),

@@ -49,12 +49,16 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   waves = std::max<int64_t>(1, waves);
   std::vector<uint64_t> tiles;
   std::vector<int64_t> empties;
-  // Per wave: d0, ndocs, T0, T1, ntiles, tab0 (into `tiles`), nempty, first
-  // empty; called after the wave's tiles, before its padding entries.
-  auto add_wave = [&](int64_t d0, int64_t ndocs, int64_t T0, int64_t T1, int64_t tab0, int64_t e0) {
+  // Per wave: d0, ndocs, T0, T1, ntiles, tab0 (into `tiles`, replaced by the
+  // first position below), nempty, first empty; called after the wave's
+  // tiles, before its padding entries.  `all_docs` counts the wave's empty
+  // documents too (the positions it takes).
+  std::vector<int64_t> wave_docs;
+  auto add_wave = [&](int64_t d0, int64_t ndocs, int64_t T0, int64_t T1, int64_t tab0, int64_t e0, int64_t all_docs) {
     const int64_t ntiles = (int64_t)tiles.size() - tab0;
     const int64_t row[kWaveInfoWords] = {d0, ndocs, T0, T1, ntiles, tab0, (int64_t)empties.size() - e0, e0};
     info.insert(info.end(), row, row + kWaveInfoWords);
+    wave_docs.push_back(all_docs);
   };
 
   const int64_t T = off[n];
@@ -86,7 +90,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
       const int64_t tab0 = (int64_t)tiles.size(), e0 = (int64_t)empties.size();
       for (int64_t d : ds) emit_doc_tiles(off[d], off[d + 1], d, tiles);
       empties.insert(empties.end(), empty_docs[(size_t)w].begin(), empty_docs[(size_t)w].end());
-      add_wave(0, (int64_t)ds.size(), 0, T, tab0, e0);
+      add_wave(0, (int64_t)ds.size(), 0, T, tab0, e0, (int64_t)(ds.size() + empty_docs[(size_t)w].size()));
       for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
     }
   } else {
@@ -107,7 +111,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
           if (off[d + 1] == off[d]) empties.push_back(d);
           else emit_doc_tiles(off[d] - T0, off[d + 1] - T0, d - d0, tiles);
         }
-        add_wave(d0, e - d0, T0, off[e], tab0, e0);
+        add_wave(d0, e - d0, T0, off[e], tab0, e0, e - d0);
         for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
         d0 = e;
       }
@@ -116,7 +120,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   // Padding waves (no documents, no tiles) up to whole workgroups.
   while ((info.size() / kWaveInfoWords) % kScanWavesPerGroup != 0) {
     const int64_t tab0 = (int64_t)tiles.size(), e0 = (int64_t)empties.size();
-    add_wave(n, 0, T, T, tab0, e0);
+    add_wave(n, 0, T, T, tab0, e0, 0);
     for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
   }
   // Every wave's entries at a fixed stride (a multiple of 8 entries, 64 B),
@@ -127,14 +131,22 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   for (int64_t w = 0; w < num_waves; ++w) longest = std::max<int64_t>(longest, info[w * kWaveInfoWords + 4]);
   stride = ((longest + kScanPrefetch + 1 + 7) / 8) * 8;
   table.assign((size_t)(num_waves * stride), kScanPastEnd);
+  // Positions in wave order: wave w's documents take [pos0, pos0 + all_docs).
+  std::vector<int64_t> block_pos;
+  int64_t pos = 0;
   for (int64_t w = 0; w < num_waves; ++w) {
     int64_t* row = &info[w * kWaveInfoWords];
     const int64_t cnt = row[4];
     std::copy(tiles.begin() + row[5], tiles.begin() + row[5] + cnt, table.begin() + w * stride);
-    row[5] = w * stride;
+    if (w % kScanWavesPerGroup == 0) block_pos.push_back(pos);
+    row[5] = pos;
+    pos += wave_docs[(size_t)w];
   }
-  // The empty-document list follows the wave rows.
+  block_pos.push_back(pos);  // == n
+  // The empty-document list, then the workgroup start positions, follow the
+  // wave rows.
   info.insert(info.end(), empties.begin(), empties.end());
+  info.insert(info.end(), block_pos.begin(), block_pos.end());
 }
 
 }  // namespace msim

@@ -410,29 +410,48 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 }
 
 // ----------------------------------------------------------------- tail form
-// One wave selects the top-k of a row of n <= kTailRow scores that other
-// workgroups of the same launch wrote with agent-scope atomic stores; they are
-// read back with coherent loads (64 per lane, all issued first).
+// The int8-query scan's fused selection (int8q_scan.hip): workgroup 0 of the
+// launch, once its own documents are done, selects each batch row's top-k,
+// one wave per row, from what every workgroup wrote with agent-scope atomic
+// stores, read back with coherent loads:
+//  * keys [n]: every document's 64-bit full key at its position (the scan's
+//    wave order; positions per workgroup are contiguous, block_pos);
+//  * bmax [nblocks]: per workgroup the largest 32-bit score key of its
+//    documents (0 for a workgroup without documents) above the launch's tag.
+// Every entry carries the launch's tag (bmax: its low 32 bits, keys: their
+// low kTailTagBits bits, tail_key_tag), and the selection reads an entry again until it
+// carries the tag: stores of other workgroups are in flight, not missing, so
+// the wait is short; a wait longer than kTailWaitTicks (an unusable device)
+// ends it with id -1 and a NaN score in every output slot of the row.
 //
 // Keys: tail_key maps a float's bits to a 32-bit order-preserving key (u ^
-// 2^31 for sign bit 0, -u otherwise, so -0 ties +0) and full keys put the
-// inverted position below it, so a larger full key is a higher score or, on
-// a tie, a lower position (the reference order).  Positions n and up get the
-// key 0, below every score's, and as k <= n are never selected.
+// 2^31 for sign bit 0, -u otherwise, so -0 ties +0; every finite float's key
+// is >= 2^23, so 0 is below every score); the full key puts 4095 - id, a -0
+// flag and the tag below it, so a larger full key is a higher score or, on a
+// tie, a lower document id (the reference order; ids are distinct, so flag
+// and tag never decide).
 //
-// T, the k-th largest of the 64 lane maxima (ties counted; a bitonic sort
-// across the wave), is at most the row's k-th largest key: every key of the
-// top-k is >= T.  Candidates (keys >= T) are counted per lane; a lane with
-// one candidate holds exactly its maximum, at the position recorded in the
-// counting pass, and writes it to `cand` at its prefix-sum slot; lanes with
-// more (ties, or the best scores crowded into one lane) store theirs in
-// order in `cand` too (a second pass over the row, taken only then).  The
-// candidates (cap at most, `cand` wave-private LDS of cap + 64 entries) are
-// ranked by counting.  More than cap candidates (cap = 0 forces it) fall
-// back to k rounds of a wave maximum over the row.
-// 1 <= k <= 64, 256 <= n (every lane's maximum is a score's, not padding).
-constexpr int kTailEPT = 64;
-constexpr int kTailRow = kTailEPT * kWave;  // 4096
+// Selection: lane l holds the block maxima of workgroups l, l + 64, ...; T,
+// the k-th largest of the 64 lane maxima (ties counted; a bitonic sort across
+// the wave), is at most the row's k-th largest score key, because k lanes
+// hold a block maximum >= T, each a different document's key.  So every key
+// of the top-k is >= T and lies in a workgroup whose maximum is >= T (a "hot"
+// workgroup, about k of them).  The hot workgroups are listed in LDS, lane i
+// loads the keys of the i-th (a second round trip, kTailBlockKeys per lane),
+// and the keys >= T are ranked by counting (by readlane when no lane holds
+// two of them, else after a compaction into LDS).  More than kTailHotMax hot
+// workgroups, one of more than kTailBlockKeys documents, or cap = 0 fall back
+// to k rounds of a wave maximum over the whole row.
+constexpr int kTailBlocks = 512;                            // workgroups at most
+constexpr int kTailBlocksPerLane = kTailBlocks / kWave;     // 8
+constexpr int kTailHotMax = 60;                             // hot workgroups of the fast path at most
+constexpr int kTailBlockKeys = 16;                          // documents per hot workgroup at most
+constexpr int kTailMaxDocs = 4096;                          // ids below 2^12
+constexpr int kTailTagBits = 19;
+constexpr uint32_t kTailTagMask = (1u << kTailTagBits) - 1u;
+constexpr uint64_t kTailWaitTicks = 10000000;               // 100 ms of s_memrealtime (100 MHz)
+// LDS of the selecting wave: candidates, then the hot-workgroup list.
+constexpr int kTailLdsBytes = kTailHotMax * kTailBlockKeys * 8 + kTailHotMax * 4;
 
 __device__ __forceinline__ uint32_t tail_key(uint32_t u) {
   const uint32_t s = (uint32_t)((int32_t)u >> 31);
@@ -444,8 +463,15 @@ __device__ __forceinline__ float tail_key_score(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : (0u - k));
 }
 
-__device__ __forceinline__ uint64_t full_key(uint32_t key, uint32_t pos) {
-  return ((uint64_t)key << 32) | (0xFFFFFFFFu - pos);
+// The key tag of a launch tag: never 0, so zeroed entries never carry it.
+__device__ __forceinline__ uint32_t tail_key_tag(uint32_t tag) { return tag % kTailTagMask + 1u; }
+
+// Full key of score s of document id < kTailMaxDocs, tagged.
+__device__ __forceinline__ uint64_t tail_full_key(float s, uint32_t id, uint32_t tag) {
+  const uint32_t u = __float_as_uint(s);
+  const uint32_t lo = (((uint32_t)(kTailMaxDocs - 1) - id) << (kTailTagBits + 1)) |
+                      ((u == 0x80000000u ? 1u : 0u) << kTailTagBits) | tail_key_tag(tag);
+  return ((uint64_t)tail_key(u) << 32) | lo;
 }
 
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int src) {
@@ -453,27 +479,11 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int src) {
          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, src);
 }
 
-// Position of register element e of a lane: 16-byte loads of 4 scores, load
-// e / 4 of lane l covering positions 4 (64 (e / 4) + l) .. + 3.
-__device__ __forceinline__ uint32_t tail_pos(int e, int lane) {
-  return (uint32_t)(4 * ((e >> 2) * kWave + lane) + (e & 3));
-}
-
-// Loads carry the agent-scope coherence bit (sc1), as an agent-scope atomic
-// load does.
-__device__ __forceinline__ v4u tail_load(__amdgpu_buffer_rsrc_t rs, int e4, int lane) {
-  return __builtin_amdgcn_raw_buffer_load_b128(rs, (e4 * kWave + lane) * 16, 0, kCoherentLoadPolicy);
-}
-
-// The score and position of a full key (+0 and -0 share one key: the score
-// is read back from the row).
-__device__ __forceinline__ void tail_write(uint64_t key, const float* row, float* out_s, int64_t* out_i) {
-  const uint32_t k32 = (uint32_t)(key >> 32);
-  const uint32_t pos = 0xFFFFFFFFu - (uint32_t)key;
-  float s = tail_key_score(k32);
-  if (k32 == 0x80000000u) s = load_score<true>(row + pos);
-  *out_s = s;
-  *out_i = (int64_t)pos;
+// The score and document id of a full key.
+__device__ __forceinline__ void tail_write(uint64_t key, float* out_s, int64_t* out_i) {
+  const uint32_t lo = (uint32_t)key;
+  *out_s = ((lo >> kTailTagBits) & 1u) ? -0.0f : tail_key_score((uint32_t)(key >> 32));
+  *out_i = (int64_t)((uint32_t)(kTailMaxDocs - 1) - (lo >> (kTailTagBits + 1)));
 }
 
 // Descending bitonic sort of one 32-bit value per lane across the wave: DPP
@@ -507,97 +517,197 @@ __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
   return v;
 }
 
+// Start position and document count of workgroups lane + 64 j (count 0
+// past nblocks): static per corpus, so the scan loads them early.
+__device__ __forceinline__ void tail_block_ranges(const int64_t* bpos, int nblocks, int (&bs)[kTailBlocksPerLane],
+                                                  int (&len)[kTailBlocksPerLane]) {
+  const int lane = lane_id();
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(bpos, (uint32_t)(nblocks + 1) * 8u);
+#pragma unroll
+  for (int j = 0; j < kTailBlocksPerLane; ++j) {
+    const int blk = lane + kWave * j;
+    bs[j] = (int)load_b64(rp, blk * 8);
+    len[j] = (int)load_b64(rp, blk * 8 + 8);
+  }
+#pragma unroll
+  for (int j = 0; j < kTailBlocksPerLane; ++j) len[j] = lane + kWave * j < nblocks ? len[j] - bs[j] : 0;
+}
+
 // Inlined into the calling kernel, whose main-loop registers are dead by
 // then (a call would save the callee-saved registers it uses to scratch).
-__device__ __forceinline__ void tail_topk(const float* row_arg, int n_arg, int k_arg, uint64_t* cand_arg,
-                                                    int cap_arg, float* out_s_arg, int64_t* out_i_arg) {
-  const float* row = reinterpret_cast<const float*>(wave_uniform64(reinterpret_cast<int64_t>(row_arg)));
+// `lds_arg`: wave-private LDS of kTailLdsBytes.  1 <= k <= min(n, 64),
+// n <= kTailMaxDocs, nblocks <= kTailBlocks; bs / len from tail_block_ranges.
+__device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64_t* bmax_arg, int nblocks_arg,
+                                          int n_arg, int k_arg, int cap_arg, uint32_t tag_arg, uint64_t* lds_arg,
+                                          const int (&bs)[kTailBlocksPerLane], const int (&len)[kTailBlocksPerLane],
+                                          float* out_s_arg, int64_t* out_i_arg) {
+  const uint64_t* keys = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(keys_arg)));
+  const uint64_t* bmax = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(bmax_arg)));
   float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
   int64_t* out_i = reinterpret_cast<int64_t*>(wave_uniform64(reinterpret_cast<int64_t>(out_i_arg)));
-  const int n = wave_uniform(n_arg), k = wave_uniform(k_arg), cap = wave_uniform(cap_arg);
-  // `cand_arg` points into LDS: address it as LDS (ds_* instructions).
+  const int nblocks = wave_uniform(nblocks_arg), n = wave_uniform(n_arg), k = wave_uniform(k_arg);
+  const int cap = wave_uniform(cap_arg);
+  const uint32_t tag = (uint32_t)wave_uniform((int)tag_arg), ktag = tail_key_tag(tag);
+  // `lds_arg` points into LDS: address it as LDS (ds_* instructions).
   typedef __attribute__((address_space(3))) uint64_t lds_u64;
-  lds_u64* cand = (lds_u64*)cand_arg;
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  lds_u64* cand = (lds_u64*)lds_arg;
+  lds_u32* hot = (lds_u32*)(cand + kTailHotMax * kTailBlockKeys);
   const int lane = lane_id();
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(row, (uint32_t)kTailRow * 4u);
-  uint32_t key[kTailEPT];
-#pragma unroll
-  for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
-    const v4u v = tail_load(rs, e4, lane);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) key[4 * e4 + c] = tail_key(v[c]);
-  }
-  if (n < kTailRow) {
-#pragma unroll
-    for (int e = 0; e < kTailEPT; ++e) key[e] = tail_pos(e, lane) < (uint32_t)n ? key[e] : 0u;
-  }
-  uint32_t mkey = 0;
-#pragma unroll
-  for (int e = 0; e < kTailEPT; e += 2) mkey = max(max(mkey, key[e]), key[e + 1]);
-  const uint32_t t = (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(mkey), k - 1);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys, (uint32_t)n * 8u);
+  const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+  auto expired = [&]() { return __builtin_amdgcn_s_memrealtime() - t_start > kTailWaitTicks; };
+  auto give_up = [&]() {
+    if (lane < k) {
+      out_s[lane] = __builtin_nanf("");
+      out_i[lane] = -1;
+    }
+  };
 
-  // Candidates per lane, and the element index of the lane's last candidate
-  // (its only one when it has one).
-  int cnt = 0, last = 0;
+  // Round trip 1: block maxima (out of range: 0), read until every one
+  // carries the tag.
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(bmax, (uint32_t)nblocks * 8u);
+  uint32_t bm[kTailBlocksPerLane];
+  for (;;) {
+    bool stale = false;
 #pragma unroll
-  for (int e = 0; e < kTailEPT; ++e) {
-    const bool take = key[e] >= t;
-    cnt += take ? 1 : 0;
-    last = take ? e : last;
+    for (int j = 0; j < kTailBlocksPerLane; ++j) {
+      const uint64_t e = load_b64_coherent(rb, (lane + kWave * j) * 8);
+      stale = stale || (len[j] > 0 && (uint32_t)e != tag);
+      bm[j] = (uint32_t)(e >> 32);
+    }
+    if (__ballot(stale) == 0) break;
+    if (expired()) {
+      give_up();
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
-  const int incl = (int)wave_inclusive_scan((uint32_t)cnt);
-  const int total = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= k
-  if (total <= cap) {
-    if (cnt == 1) cand[incl - 1] = full_key(mkey, tail_pos(last, lane));
-    if (__ballot(cnt > 1) != 0) {
-      // Lanes with several candidates store them all, in position order.
-      if (cnt > 1) {
-        int slot = incl - cnt;
-        const int spare = cap + lane;
+  uint32_t lmax = 0;
 #pragma unroll
-        for (int e = 0; e < kTailEPT; ++e) {
-          const bool take = key[e] >= t;
-          cand[take ? slot : spare] = full_key(key[e], tail_pos(e, lane));
-          slot += take ? 1 : 0;
+  for (int j = 0; j < kTailBlocksPerLane; ++j) lmax = max(lmax, bm[j]);
+  // T >= 1: blocks without documents (maximum 0) are never hot.
+  const uint32_t t = max(1u, (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(lmax), k - 1));
+  int nh = 0;
+  bool wide = false;
+#pragma unroll
+  for (int j = 0; j < kTailBlocksPerLane; ++j) {
+    nh += bm[j] >= t ? 1 : 0;
+    wide = wide || (bm[j] >= t && len[j] > kTailBlockKeys);
+  }
+  const int incl = (int)wave_inclusive_scan((uint32_t)nh);
+  const int nhot = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= 1
+  if (cap > 0 && nhot <= kTailHotMax && __ballot(wide) == 0) {
+    int o = incl - nh;
+#pragma unroll
+    for (int j = 0; j < kTailBlocksPerLane; ++j)
+      if (bm[j] >= t) hot[o++] = ((uint32_t)bs[j] << 8) | (uint32_t)len[j];
+    wave_sync_lds();
+    // Round trip 2: the keys of hot workgroup h go to lanes 8 (h % 8) ..
+    // 8 (h % 8) + 7, two each, in round h / 8 (registers x[2 (h / 8)] and
+    // x[2 (h / 8) + 1]; past a workgroup's count: out of range, key 0), so
+    // that each load instruction reads eight runs of 16 bytes; read again
+    // until every key carries the tag.
+    constexpr int kRounds = kTailBlockKeys / 2;
+    static_assert(kRounds * 8 >= kTailHotMax, "eight hot workgroups per round");
+    int start[kRounds], cnt[kRounds];
+    const int sub = 2 * (lane & 7);
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int h = 8 * r + (lane >> 3);
+      const uint32_t hb = h < nhot ? (uint32_t)hot[h] : 0u;
+      start[r] = (int)(hb >> 8) + sub;
+      cnt[r] = (int)(hb & 255u) - sub;  // keys of this lane's pair inside the workgroup: min(2, cnt)
+    }
+    uint64_t x[kTailBlockKeys];
+    for (;;) {
+      bool stale = false;
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const bool in = e < cnt[r];
+          x[2 * r + e] = load_b64_coherent(rk, in ? (start[r] + e) * 8 : n * 8);
+          stale = stale || (in && ((uint32_t)x[2 * r + e] & kTailTagMask) != ktag);
         }
       }
-    }
-    wave_sync_lds();
-    if (total <= kWave) {
-      // One candidate per lane, ranked by readlane.
-      const uint64_t x = lane < total ? (uint64_t)cand[lane] : 0ull;
-      int r = 0;
-#pragma unroll 4
-      for (int j = 0; j < total; ++j) r += readlane_u64(x, j) > x ? 1 : 0;
-      if (lane < total && r < k) tail_write(x, row, out_s + r, out_i + r);
-    } else {
-      for (int s = lane; s < total; s += kWave) {
-        const uint64_t x = cand[s];
-        int r = 0;
-        for (int q = 0; q < total; ++q) r += cand[q] > x ? 1 : 0;
-        if (r < k) tail_write(x, row, out_s + r, out_i + r);
+      if (__ballot(stale) == 0) break;
+      if (expired()) {
+        give_up();
+        return;
       }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // Candidates: keys >= T (at least k of them).
+    int c2 = 0;
+    uint64_t y = 0;
+#pragma unroll
+    for (int q = 0; q < kTailBlockKeys; ++q) {
+      const bool take = (uint32_t)(x[q] >> 32) >= t;
+      c2 += take ? 1 : 0;
+      y = take ? x[q] : y;
+    }
+    if (__ballot(c2 > 1) == 0) {
+      // At most one candidate per lane: rank by readlane over the lanes
+      // holding one (full keys are distinct).
+      uint64_t m = __ballot(c2 == 1);
+      int r = 0;
+      while (m != 0) {
+        const int j = (int)__builtin_ctzll(m);
+        m &= m - 1;
+        r += readlane_u64(y, j) > y ? 1 : 0;
+      }
+      if (c2 == 1 && r < k) tail_write(y, out_s + r, out_i + r);
+      wave_sync_lds();
+      return;
+    }
+    const int incl2 = (int)wave_inclusive_scan((uint32_t)c2);
+    const int total = __builtin_amdgcn_readlane(incl2, kWave - 1);  // >= k
+    int o2 = incl2 - c2;
+#pragma unroll
+    for (int q = 0; q < kTailBlockKeys; ++q)
+      if ((uint32_t)(x[q] >> 32) >= t) cand[o2++] = x[q];
+    wave_sync_lds();
+    for (int s = lane; s < total; s += kWave) {
+      const uint64_t z = cand[s];
+      int r = 0;
+      for (int q = 0; q < total; ++q) r += cand[q] > z ? 1 : 0;
+      if (r < k) tail_write(z, out_s + r, out_i + r);
     }
     wave_sync_lds();
     return;
   }
-  // k rounds over the row (read again each round): the largest full key
-  // below the previous round's.
+  // Fallback: wait until every key of the row carries the tag, then k
+  // rounds over the row (read again each round): the largest full key below
+  // the previous round's.
+  const int chunks = (n + 2 * kWave - 1) / (2 * kWave);
+  for (;;) {
+    bool stale = false;
+#pragma unroll 1
+    for (int i = 0; i < chunks; ++i) {
+      const int p = 2 * (i * kWave + lane);
+      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rk, p * 8, 0, kCoherentLoadPolicy);
+      stale = stale || (p < n && (v[0] & kTailTagMask) != ktag) || (p + 1 < n && (v[2] & kTailTagMask) != ktag);
+    }
+    if (__ballot(stale) == 0) break;
+    if (expired()) {
+      give_up();
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
   uint64_t prev = ~0ull;
   for (int r = 0; r < k; ++r) {
     uint64_t best = 0;
 #pragma unroll 1
-    for (int e4 = 0; e4 < kTailEPT / 4; ++e4) {
-      const v4u v = tail_load(rs, e4, lane);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t pos = tail_pos(4 * e4 + c, lane);
-        const uint64_t f = full_key(pos < (uint32_t)n ? tail_key(v[c]) : 0u, pos);
-        best = (f < prev && f > best) ? f : best;
-      }
+    for (int i = 0; i < chunks; ++i) {
+      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rk, (i * kWave + lane) * 16, 0, kCoherentLoadPolicy);
+      const uint64_t a = ((uint64_t)v[1] << 32) | v[0], b = ((uint64_t)v[3] << 32) | v[2];
+      best = (a < prev && a > best) ? a : best;
+      best = (b < prev && b > best) ? b : best;
     }
     const uint64_t top = wave_max_u64(best);
-    if (lane == 0) tail_write(top, row, out_s + r, out_i + r);
+    if (lane == 0) tail_write(top, out_s + r, out_i + r);
     prev = top;
   }
 }

@@ -2,8 +2,11 @@
 // build_scan_tables (scan_tables.cpp), both partition modes: every token of
 // every non-empty document lies in a tile of its own document, exactly one
 // tile per document is marked last and ends at the document end, every empty
-// document is listed once, tile slots are padded, and the wave count is a
-// multiple of the workgroup size.  build_score_tables (score_tables.cpp),
+// document is listed once, tile slots are padded, the wave count is a
+// multiple of the workgroup size, and the fused selection's positions (each
+// wave's empty documents, then its documents in tile order, from the wave's
+// first position) number the documents 0..n-1 once each, with every
+// workgroup's first position in the block_pos list after the empty list.  build_score_tables (score_tables.cpp),
 // documents or candidate targets (with duplicates): every target's tokens are
 // covered by its tiles in order, exactly once, its last tile flagged, an empty
 // target gets one empty tile, and every wave ends with a padding entry.
@@ -21,18 +24,34 @@ int main() {
       int64_t waves = 1 + rng() % 64;
       std::vector<int64_t> info; std::vector<uint64_t> table; int64_t stride, nw;
       msim::build_scan_tables(off.data(), n, waves, contiguous, info, table, stride, nw);
-      std::vector<int> seen_tok(off[n], 0), seen_empty(n, 0), doc_tiles_last(n, 0);
+      std::vector<int> seen_tok(off[n], 0), seen_empty(n, 0), doc_tiles_last(n, 0), pos_of(n, -1), doc_at(n, -1);
+      int64_t total_empty = 0;
+      for (int64_t w = 0; w < nw; ++w) total_empty += info[w * 8 + 6];
+      const int64_t* block_pos = &info[nw * 8 + total_empty];
+      if ((int64_t)info.size() != nw * 8 + total_empty + nw / 4 + 1 || block_pos[nw / 4] != n) { printf("BAD block_pos size\n"); return 1; }
       for (int64_t w = 0; w < nw; ++w) {
         const int64_t* r = &info[w * 8];
+        if (w % 4 == 0 && block_pos[w / 4] != r[5]) { printf("BAD block_pos\n"); return 1; }
+        int64_t next = r[5];
+        auto place = [&](int64_t doc) -> bool {
+          if (next < 0 || next >= n || doc_at[next] >= 0 || pos_of[doc] >= 0) return false;
+          doc_at[next] = (int)doc; pos_of[doc] = (int)next; ++next; return true;
+        };
+        for (int64_t e = 0; e < r[6]; ++e) if (!place(info[nw * 8 + r[7] + e])) { printf("BAD empty position\n"); return 1; }
         for (int64_t i = 0; i < r[4]; ++i) {
-          uint64_t e = table[r[5] + i]; int64_t start = (int64_t)(e & 0xFFFFFFFFu) + r[2];
+          uint64_t e = table[w * stride + i];
+          if ((e >> 37) & 1) if (!place((int64_t)(e >> 40) + r[0])) { printf("BAD doc position\n"); return 1; }
+        }
+        if (w + 1 < nw && next != info[(w + 1) * 8 + 5]) { printf("BAD next position\n"); return 1; }
+        for (int64_t i = 0; i < r[4]; ++i) {
+          uint64_t e = table[w * stride + i]; int64_t start = (int64_t)(e & 0xFFFFFFFFu) + r[2];
           uint32_t hi = (uint32_t)(e >> 32); int rows = (hi & 31) + 1; bool last = (hi >> 5) & 1; int64_t doc = (hi >> 8) + r[0];
           if (doc < 0 || doc >= n || start < off[doc] || start + rows > off[doc + 1]) { printf("BAD tile w%ld\n", (long)w); return 1; }
           for (int t = 0; t < rows; ++t) seen_tok[start + t]++;
           if (last) doc_tiles_last[doc]++;
           if (last != (start + rows == off[doc + 1])) { printf("BAD last\n"); return 1; }
         }
-        for (int64_t i = r[4]; i < stride; ++i) if (table[r[5] + i] != msim::kScanPastEnd) { printf("BAD pad\n"); return 1; }
+        for (int64_t i = r[4]; i < stride; ++i) if (table[w * stride + i] != msim::kScanPastEnd) { printf("BAD pad\n"); return 1; }
         for (int64_t e = 0; e < r[6]; ++e) seen_empty[info[nw * 8 + r[7] + e]]++;
       }
       for (int d = 0; d < n; ++d) {
@@ -40,6 +59,7 @@ int main() {
         if (empty ? (seen_empty[d] != 1 || doc_tiles_last[d]) : (doc_tiles_last[d] != 1 || seen_empty[d])) { printf("BAD doc %d\n", d); return 1; }
       }
       for (int64_t t = 0; t < off[n]; ++t) if (seen_tok[t] < 1) { printf("BAD token %ld\n", (long)t); return 1; }
+      for (int d = 0; d < n; ++d) if (pos_of[d] < 0) { printf("BAD unplaced doc %d\n", d); return 1; }
       if (nw % 4) { printf("BAD nw\n"); return 1; }
     }
   }
