@@ -144,8 +144,8 @@ int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t 
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): msim_int4_topk_int8q_async with the same arguments and
  * results, whose scratch memory (quantised query, score rows, the fused
- * selection's key rows, block maxima and launch counter) is a fixed
- * 461,056-byte device array per GPU instead of
+ * selection's key rows, workgroup records and launch counter) is a fixed
+ * 526,592-byte device array per GPU instead of
  * handle workspaces, so the call allocates nothing.  Limits: 1 <= batch *
  * query_tokens <= 128, k <= 32, and either the fused selection applies
  * (256 <= num_docs <= 4096, batch <= 8, msim_set_fused_topk mode 1 or 2) or

@@ -325,25 +325,25 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
   if (k > 0) {
     // Fill kernels, not memsets, so that a captured call records no memset
     // node; they run once per allocation: the launch counter starts at 0 and
-    // the key and block-maximum rows hold no tag of a later launch.
+    // the key rows and workgroup records hold no tag of a later launch.
     if (h->tail_epoch.ptr == nullptr) {
       h->tail_epoch.ensure(256, "hipMalloc scan launch counter");
       check_hip(launch_fill_f32(h->tail_epoch.as<float>(), 1, 0.0f, stream), "zero scan launch counter");
     }
     const int64_t rows = std::min(batch, std::max<int64_t>(1, kScanPassRows / query_tokens));
     const size_t key_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailRow);
-    const size_t bmax_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailBlocks);
+    const size_t rec_bytes = sizeof(uint64_t) * (size_t)(rows * 3 * kScanTailBlocks);
     if (h->tail_keys.cap < key_bytes) {
       h->tail_keys.ensure(key_bytes, "hipMalloc scan tail key rows");
       check_hip(launch_fill_f32(h->tail_keys.as<float>(), (int64_t)(key_bytes / 4), 0.0f, stream), "zero scan tail key rows");
     }
-    if (h->tail_bmax.cap < bmax_bytes) {
-      h->tail_bmax.ensure(bmax_bytes, "hipMalloc scan tail block maxima");
-      check_hip(launch_fill_f32(h->tail_bmax.as<float>(), (int64_t)(bmax_bytes / 4), 0.0f, stream),
-                "zero scan tail block maxima");
+    if (h->tail_rec.cap < rec_bytes) {
+      h->tail_rec.ensure(rec_bytes, "hipMalloc scan tail workgroup records");
+      check_hip(launch_fill_f32(h->tail_rec.as<float>(), (int64_t)(rec_bytes / 4), 0.0f, stream),
+                "zero scan tail workgroup records");
     }
     a.tail_keys = h->tail_keys.as<uint64_t>();
-    a.tail_bmax = h->tail_bmax.as<uint64_t>();
+    a.tail_rec = h->tail_rec.as<uint64_t>();
     a.topk_k = (int32_t)k;
     a.tail_cap = g_fused_topk == 2 ? 0 : INT32_MAX;
     a.epoch = h->tail_epoch.as<uint32_t>();

@@ -113,8 +113,8 @@ struct msim_int4_docs {
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
   // Scan with fused top-k: launch counter, key rows of kScanTailRow tagged
-  // 64-bit keys and block-maximum rows of kScanTailBlocks tagged entries.
-  msim::DeviceBuffer tail_epoch, tail_keys, tail_bmax;
+  // 64-bit keys and workgroup records (3 x kScanTailBlocks tagged words per row).
+  msim::DeviceBuffer tail_epoch, tail_keys, tail_rec;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
@@ -123,7 +123,7 @@ struct msim_int4_docs {
   }
   uint64_t workspace_bytes() const {
     return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap + top_indices.cap +
-           rowmax.cap + wave_info.cap + tile_table.cap + tail_epoch.cap + tail_keys.cap + tail_bmax.cap + ws.bytes();
+           rowmax.cap + wave_info.cap + tile_table.cap + tail_epoch.cap + tail_keys.cap + tail_rec.cap + ws.bytes();
   }
 };
 

@@ -175,19 +175,26 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   float* qs = s_qscale[wave];
   // Fused selection: documents take positions pos0, pos0 + 1, ... (the
   // wave's empty documents, then the others in tile order); per batch row
-  // the largest score key of the wave's documents.
-  __shared__ uint32_t s_bmax[kScanWaves][kScanTailMaxRows];
+  // the three largest full keys of the wave's documents (0: none).
+  __shared__ uint64_t s_top[kScanWaves][kScanTailMaxRows][3];
   const int pos0 = (int)info[5];
   int nfin = 0;
   uint32_t tag = 0;  // the launch's tag (fused), read below
-  if (fused && lane < kScanTailMaxRows) s_bmax[wave][lane] = 0u;
-  // Score v of document doc for batch row b, at position pos.
-  auto emit = [&](int b, int64_t doc, int pos, float v) {
+  if (fused && lane < kScanTailMaxRows * 3) (&s_top[wave][0][0])[lane] = 0ull;
+  // Score v of document doc for batch row b, at position pos; `rank` also
+  // enters it in the wave's top three of row b (one lane per row at a time).
+  auto emit = [&](int b, int64_t doc, int pos, float v, bool rank = true) {
     if constexpr (fused) {
       const uint64_t key = tail_full_key(v, (uint32_t)doc, tag);
       __hip_atomic_store(p.tail_keys + (int64_t)b * kScanTailRow + pos, key, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-      atomicMax(&s_bmax[wave][b], (uint32_t)(key >> 32));
+      if (rank) {
+        uint64_t* t3 = s_top[wave][b];
+        const uint64_t a0 = t3[0], a1 = t3[1], a2 = t3[2];
+        t3[0] = max(a0, key);
+        t3[1] = max(a1, min(a0, key));
+        t3[2] = max(a2, min(a1, key));
+      }
     } else {
       scores[(int64_t)b * p.score_stride + doc] = v;
     }
@@ -473,32 +480,53 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (!fused) vm_wait_lds<0>();
 
   // Empty documents score 0 (the wave's entries of the empty-document list).
+  // Fused: they all score 0, so the wave's three lowest ids (its first
+  // entries) are the only ones that can enter its top three.
   for (int e = lane; e < nempty; e += kWave) {
     const int64_t doc = wave_info_ptr[p.num_waves * kWaveInfoWords + e0 + e];
-    for (int b = 0; b < p.batch; ++b) emit(b, doc, pos0 + e, 0.0f);
+    for (int b = 0; b < p.batch; ++b) emit(b, doc, pos0 + e, 0.0f, false);
+  }
+  if (fused && lane == 0) {
+    for (int e = 0; e < min(nempty, 3); ++e) {
+      const int64_t doc = wave_info_ptr[p.num_waves * kWaveInfoWords + e0 + e];
+      for (int b = 0; b < p.batch; ++b) emit(b, doc, pos0 + e, 0.0f);
+    }
   }
   if constexpr (!fused) return;
 
-  // Fused selection.  The workgroup's block maxima (one thread per batch
-  // row, after an LDS-only barrier: the key stores stay in flight), tagged.
+  // Fused selection.  The workgroup's record per batch row (one thread per
+  // row, after an LDS-only barrier: the key stores stay in flight): its two
+  // largest full keys and the third one's score key, each word tagged.
   // Every workgroup but 0 is then done; workgroup 0 selects (each of its
   // waves once its own tile ring has drained).
   int bs[kTailBlocksPerLane], blen[kTailBlocksPerLane];
   if (blockIdx.x == 0) tail_block_ranges(p.block_pos, (int)gridDim.x, bs, blen);
   group_sync_lds();
   if ((int)threadIdx.x < p.batch) {
-    uint32_t bm = 0;
+    uint64_t a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
-    for (int w = 0; w < kScanWaves; ++w) bm = max(bm, s_bmax[w][threadIdx.x]);
-    __hip_atomic_store(p.tail_bmax + (int64_t)threadIdx.x * kScanTailBlocks + blockIdx.x, ((uint64_t)bm << 32) | tag,
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int w = 0; w < kScanWaves; ++w) {
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const uint64_t key = s_top[w][threadIdx.x][i];
+        const uint64_t m0 = min(a0, key), m1 = min(a1, m0);
+        a0 = max(a0, key);
+        a1 = max(a1, m0);
+        a2 = max(a2, m1);
+      }
+    }
+    const uint64_t ktag = tail_key_tag(tag);
+    uint64_t* rec = p.tail_rec + (int64_t)threadIdx.x * 3 * kScanTailBlocks + blockIdx.x;
+    __hip_atomic_store(rec, a0 != 0 ? a0 : ktag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + kScanTailBlocks, a1 != 0 ? a1 : ktag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + 2 * kScanTailBlocks, ((a2 >> 32) << 32) | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   vm_wait_lds<0>();
   if (blockIdx.x != 0) return;
   // Wave w selects batch rows w, w + 4, ... in its tile ring's LDS.
   uint64_t* lds = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
   for (int b = wave; b < p.batch; b += kScanWaves)
-    tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_bmax + (int64_t)b * kScanTailBlocks, (int)gridDim.x,
+    tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_rec + (int64_t)b * 3 * kScanTailBlocks, (int)gridDim.x,
               (int)p.num_docs, p.topk_k, p.tail_cap, tag, lds, bs, blen, p.top_scores + (int64_t)b * p.topk_k,
               p.top_ids + (int64_t)b * p.topk_k);
   // Every workgroup read the counter at its start, before its block maxima
@@ -543,7 +571,7 @@ hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t str
        args.num_docs < kScanTailMinDocs || args.batch > kScanTailMaxRows ||
        args.num_waves > (int64_t)kScanWaves * kScanTailBlocks || args.epoch == nullptr ||
        args.top_scores == nullptr || args.top_ids == nullptr || args.tail_keys == nullptr ||
-       args.tail_bmax == nullptr || args.block_pos == nullptr))
+       args.tail_rec == nullptr || args.block_pos == nullptr))
     return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;

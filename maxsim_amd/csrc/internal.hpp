@@ -93,13 +93,13 @@ struct ScanArgs {
   // kScanTailMaxDocs, num_waves <= 4 * kScanTailBlocks): the launch's tag is
   // *epoch + 1; every document's score goes write-through, as a tagged 64-bit
   // selection key (tail_full_key), to its wave-order position of tail_keys
-  // [batch, kScanTailRow]; every workgroup writes the largest 32-bit score key
-  // of its documents per batch row, above the tag, to tail_bmax [batch,
-  // kScanTailBlocks]; workgroup 0 waits until its reads carry the tag, selects
-  // the top-k of every batch row into top_scores / top_ids [batch, topk_k] and
-  // stores the tag to *epoch.  tail_keys and tail_bmax hold no entry with a
-  // later launch's tag (zero them when allocated).  block_pos [num_waves / 4 +
-  // 1] holds each workgroup's first position (then num_docs).
+  // [batch, kScanTailRow]; every workgroup writes a tagged record per batch
+  // row to tail_rec [batch, 3, kScanTailBlocks] (its two largest keys, the
+  // third one's score key); workgroup 0 waits until its reads carry the tag,
+  // selects the top-k of every batch row into top_scores / top_ids [batch,
+  // topk_k] and stores the tag to *epoch.  tail_keys and tail_rec hold no
+  // entry with a later launch's tag (zero them when allocated).  block_pos
+  // [num_waves / 4 + 1] holds each workgroup's first position (then num_docs).
   int32_t topk_k;
   int32_t tail_cap;             // 0 forces the selection's k-round path
   int64_t num_docs;
@@ -107,7 +107,7 @@ struct ScanArgs {
   float* top_scores;
   int64_t* top_ids;
   uint64_t* tail_keys;
-  uint64_t* tail_bmax;
+  uint64_t* tail_rec;
   const int64_t* block_pos;
 };
 constexpr int kScanTailMaxK = 32;

@@ -1,7 +1,7 @@
 // noalloc.hip -- msim_int4_topk_int8q_noalloc: the int8-query search of
 // msim_int4_topk_int8q_async with its scratch memory (quantised query, score
-// rows of an unfused call, the fused selection's key rows, block maxima and
-// launch counter) in one fixed device array instead of handle workspaces, so
+// rows of an unfused call, the fused selection's key rows, workgroup records
+// and launch counter) in one fixed device array instead of handle workspaces, so
 // a call allocates nothing.  For callers that cannot allocate device memory
 // (code under HIP graph capture, tight serving loops).
 //
@@ -29,10 +29,10 @@ constexpr size_t kQscaleOff = kQpackOff + kNoallocQueryRows * 128;
 constexpr size_t kQbiasOff = kQscaleOff + kNoallocQueryRows * 4;
 constexpr size_t kScoresOff = kQbiasOff + kNoallocQueryRows * 4;  // score rows of an unfused call
 constexpr size_t kKeysOff = kScoresOff + kNoallocScoreFloats * 4;  // fused: key rows
-constexpr size_t kBmaxOff = kKeysOff + kScanTailMaxRows * kScanTailRow * 8;  // fused: block maxima
-constexpr size_t kEpochOff = kBmaxOff + kScanTailMaxRows * kScanTailBlocks * 8;  // fused: launch counter
-constexpr size_t kScratchBytes = kEpochOff + 256;  // 461,056 bytes
-static_assert(kScoresOff % 256 == 0 && kKeysOff % 256 == 0 && kBmaxOff % 256 == 0 && kEpochOff % 256 == 0,
+constexpr size_t kRecOff = kKeysOff + kScanTailMaxRows * kScanTailRow * 8;  // fused: workgroup records
+constexpr size_t kEpochOff = kRecOff + kScanTailMaxRows * 3 * kScanTailBlocks * 8;  // fused: launch counter
+constexpr size_t kScratchBytes = kEpochOff + 256;  // 526,592 bytes
+static_assert(kScoresOff % 256 == 0 && kKeysOff % 256 == 0 && kRecOff % 256 == 0 && kEpochOff % 256 == 0,
               "aligned scratch regions");
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -102,7 +102,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
     a.batch = (int32_t)batch;
     if (fused) {
       a.tail_keys = reinterpret_cast<uint64_t*>(base + kKeysOff);
-      a.tail_bmax = reinterpret_cast<uint64_t*>(base + kBmaxOff);
+      a.tail_rec = reinterpret_cast<uint64_t*>(base + kRecOff);
       a.topk_k = (int32_t)k;
       a.tail_cap = mode == 2 ? 0 : INT32_MAX;
       a.epoch = reinterpret_cast<uint32_t*>(base + kEpochOff);

@@ -416,13 +416,15 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // stores, read back with coherent loads:
 //  * keys [n]: every document's 64-bit full key at its position (the scan's
 //    wave order; positions per workgroup are contiguous, block_pos);
-//  * bmax [nblocks]: per workgroup the largest 32-bit score key of its
-//    documents (0 for a workgroup without documents) above the launch's tag.
-// Every entry carries the launch's tag (bmax: its low 32 bits, keys: their
-// low kTailTagBits bits, tail_key_tag), and the selection reads an entry again until it
-// carries the tag: stores of other workgroups are in flight, not missing, so
-// the wait is short; a wait longer than kTailWaitTicks (an unusable device)
-// ends it with id -1 and a NaN score in every output slot of the row.
+//  * rec [3][kTailBlocks]: per workgroup (block) its largest and second largest
+//    full keys (none: key 0) and, above the tag, the third largest's 32-bit
+//    score key.
+// Every entry carries the launch's tag (rec[2]: its low 32 bits, full keys:
+// their low kTailTagBits bits, tail_key_tag), and the selection reads an
+// entry again until it carries the tag: stores of other workgroups are in
+// flight, not missing, so the wait is short; a wait longer than
+// kTailWaitTicks (an unusable device) ends it with id -1 and a NaN score in
+// every output slot of the row.
 //
 // Keys: tail_key maps a float's bits to a 32-bit order-preserving key (u ^
 // 2^31 for sign bit 0, -u otherwise, so -0 ties +0; every finite float's key
@@ -431,27 +433,30 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // tie, a lower document id (the reference order; ids are distinct, so flag
 // and tag never decide).
 //
-// Selection: lane l holds the block maxima of workgroups l, l + 64, ...; T,
-// the k-th largest of the 64 lane maxima (ties counted; a bitonic sort across
-// the wave), is at most the row's k-th largest score key, because k lanes
-// hold a block maximum >= T, each a different document's key.  So every key
-// of the top-k is >= T and lies in a workgroup whose maximum is >= T (a "hot"
-// workgroup, about k of them).  The hot workgroups are listed in LDS, lane i
-// loads the keys of the i-th (a second round trip, kTailBlockKeys per lane),
-// and the keys >= T are ranked by counting (by readlane when no lane holds
-// two of them, else after a compaction into LDS).  More than kTailHotMax hot
-// workgroups, one of more than kTailBlockKeys documents, or cap = 0 fall back
-// to k rounds of a wave maximum over the whole row.
+// Selection: lane l holds the records of blocks l, l + 64, ...; T, the k-th
+// largest of the 64 lane maxima (ties counted; a radix selection by ballot
+// counts), is at most the row's k-th largest score key, because k lanes hold a
+// block maximum >= T, each a different document's key.  So every key of the
+// top-k is >= T and lies in a block whose maximum is >= T (a "hot" block).
+// A hot block whose third score key is below T has all its keys >= T in its
+// record; a deeper one has its keys loaded (eight lanes per block, two keys
+// each, a second round trip).  The keys >= T are appended to a candidate
+// list in LDS and each one's rank counted against the whole list (broadcast
+// LDS reads).  More than kTailHotMax hot blocks, a deep one of more than
+// kTailBlockKeys documents, or cap = 0 fall back to k rounds of a wave
+// maximum over the whole row.
 constexpr int kTailBlocks = 512;                            // workgroups at most
 constexpr int kTailBlocksPerLane = kTailBlocks / kWave;     // 8
-constexpr int kTailHotMax = 60;                             // hot workgroups of the fast path at most
-constexpr int kTailBlockKeys = 16;                          // documents per hot workgroup at most
+constexpr int kTailHotMax = 48;                             // hot blocks of the fast path at most
+constexpr int kTailBlockKeys = 16;                          // documents per deep block at most
 constexpr int kTailMaxDocs = 4096;                          // ids below 2^12
 constexpr int kTailTagBits = 19;
 constexpr uint32_t kTailTagMask = (1u << kTailTagBits) - 1u;
 constexpr uint64_t kTailWaitTicks = 10000000;               // 100 ms of s_memrealtime (100 MHz)
-// LDS of the selecting wave: candidates, then the hot-workgroup list.
-constexpr int kTailLdsBytes = kTailHotMax * kTailBlockKeys * 8 + kTailHotMax * 4;
+// LDS of the selecting wave: candidates (at most kTailBlockKeys per hot
+// block, then eight zero keys), then the list of deep blocks.
+constexpr int kTailCandMax = kTailHotMax * kTailBlockKeys;
+constexpr int kTailLdsBytes = (kTailCandMax + 8) * 8 + kWave * 4;
 
 __device__ __forceinline__ uint32_t tail_key(uint32_t u) {
   const uint32_t s = (uint32_t)((int32_t)u >> 31);
@@ -486,37 +491,6 @@ __device__ __forceinline__ void tail_write(uint64_t key, float* out_s, int64_t* 
   *out_i = (int64_t)((uint32_t)(kTailMaxDocs - 1) - (lo >> (kTailTagBits + 1)));
 }
 
-// Descending bitonic sort of one 32-bit value per lane across the wave: DPP
-// exchanges for lane distances 1, 2, 4 and 8, ds_swizzle for 16, a
-// bpermute for 32.
-__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
-  const int lane = lane_id();
-  auto partner = [&](uint32_t x, int d) -> uint32_t {
-    switch (d) {
-      case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-      case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-      case 4: {
-        // lanes with bit 2 clear (banks 0, 2) read l + 4, the others l - 4
-        const int t = __builtin_amdgcn_update_dpp(0, (int)x, 0x104, 0xF, 0x5, false);  // row_shl:4
-        return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)x, 0x114, 0xF, 0xA, false);  // row_shr:4
-      }
-      case 8: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);  // row_ror:8
-      case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F);  // xor 16 within each half
-      default: return (uint32_t)__shfl_xor((int)x, 32);
-    }
-  };
-#pragma unroll
-  for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-    for (int d = size >> 1; d > 0; d >>= 1) {
-      const uint32_t p = partner(v, d);
-      const bool keep_max = ((lane & d) == 0) == ((lane & size) == 0);
-      v = keep_max ? max(v, p) : min(v, p);
-    }
-  }
-  return v;
-}
-
 // Start position and document count of workgroups lane + 64 j (count 0
 // past nblocks): static per corpus, so the scan loads them early.
 __device__ __forceinline__ void tail_block_ranges(const int64_t* bpos, int nblocks, int (&bs)[kTailBlocksPerLane],
@@ -537,12 +511,12 @@ __device__ __forceinline__ void tail_block_ranges(const int64_t* bpos, int nbloc
 // then (a call would save the callee-saved registers it uses to scratch).
 // `lds_arg`: wave-private LDS of kTailLdsBytes.  1 <= k <= min(n, 64),
 // n <= kTailMaxDocs, nblocks <= kTailBlocks; bs / len from tail_block_ranges.
-__device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64_t* bmax_arg, int nblocks_arg,
+__device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64_t* rec_arg, int nblocks_arg,
                                           int n_arg, int k_arg, int cap_arg, uint32_t tag_arg, uint64_t* lds_arg,
                                           const int (&bs)[kTailBlocksPerLane], const int (&len)[kTailBlocksPerLane],
                                           float* out_s_arg, int64_t* out_i_arg) {
   const uint64_t* keys = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(keys_arg)));
-  const uint64_t* bmax = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(bmax_arg)));
+  const uint64_t* rec = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(rec_arg)));
   float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
   int64_t* out_i = reinterpret_cast<int64_t*>(wave_uniform64(reinterpret_cast<int64_t>(out_i_arg)));
   const int nblocks = wave_uniform(nblocks_arg), n = wave_uniform(n_arg), k = wave_uniform(k_arg);
@@ -552,7 +526,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   typedef __attribute__((address_space(3))) uint64_t lds_u64;
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
   lds_u64* cand = (lds_u64*)lds_arg;
-  lds_u32* hot = (lds_u32*)(cand + kTailHotMax * kTailBlockKeys);
+  lds_u32* deep_list = (lds_u32*)(cand + kTailCandMax + 8);
   const int lane = lane_id();
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys, (uint32_t)n * 8u);
   const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
@@ -563,20 +537,31 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
       out_i[lane] = -1;
     }
   };
+  auto rank_below = [&](uint64_t mask) -> int {  // set bits of mask below this lane
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+  };
+  auto key_current = [&](uint64_t x) { return ((uint32_t)x & kTailTagMask) == ktag; };
 
-  // Round trip 1: block maxima (out of range: 0), read until every one
-  // carries the tag.
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(bmax, (uint32_t)nblocks * 8u);
-  uint32_t bm[kTailBlocksPerLane];
+  // Round trip 1: the records (out of range: 0; a block without documents
+  // still writes one), read until every word carries the tag.
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(rec, (uint32_t)(3 * kTailBlocks * 8));
+  uint64_t w0[kTailBlocksPerLane], w1[kTailBlocksPerLane];
+  uint32_t third[kTailBlocksPerLane];
   for (;;) {
-    bool stale = false;
+    uint32_t stale = 0;
 #pragma unroll
     for (int j = 0; j < kTailBlocksPerLane; ++j) {
-      const uint64_t e = load_b64_coherent(rb, (lane + kWave * j) * 8);
-      stale = stale || (len[j] > 0 && (uint32_t)e != tag);
-      bm[j] = (uint32_t)(e >> 32);
+      const int blk = lane + kWave * j;
+      const uint64_t a = load_b64_coherent(rr, blk * 8);
+      const uint64_t b = load_b64_coherent(rr, (kTailBlocks + blk) * 8);
+      const uint64_t c = load_b64_coherent(rr, (2 * kTailBlocks + blk) * 8);
+      const bool in = blk < nblocks;
+      w0[j] = in ? a : 0ull;
+      w1[j] = in ? b : 0ull;
+      third[j] = in ? (uint32_t)(c >> 32) : 0u;
+      stale |= (uint32_t)in & ((uint32_t)!key_current(a) | (uint32_t)!key_current(b) | (uint32_t)((uint32_t)c != tag));
     }
-    if (__ballot(stale) == 0) break;
+    if (__ballot(stale != 0) == 0) break;
     if (expired()) {
       give_up();
       return;
@@ -585,94 +570,109 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   }
   uint32_t lmax = 0;
 #pragma unroll
-  for (int j = 0; j < kTailBlocksPerLane; ++j) lmax = max(lmax, bm[j]);
-  // T >= 1: blocks without documents (maximum 0) are never hot.
-  const uint32_t t = max(1u, (uint32_t)__builtin_amdgcn_readlane((int)wave_sort_desc_u32(lmax), k - 1));
-  int nh = 0;
+  for (int j = 0; j < kTailBlocksPerLane; ++j) lmax = max(lmax, (uint32_t)(w0[j] >> 32));
+  // T: the largest value that k lane maxima reach, bit by bit from the top
+  // (ballot counts); T >= 1, so blocks without documents (maximum 0) are
+  // never hot.
+  uint32_t t = 0;
+#pragma unroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = t | (1u << bit);
+    t = __popcll(__ballot(lmax >= c)) >= k ? c : t;
+  }
+  t = max(t, 1u);
+  // Hot blocks (maximum >= T), deep ones (a third key >= T, so hot too; listed
+  // in LDS for the second round trip) and the record keys >= T of the others,
+  // counted by one scan: candidates in bits 20.., hot blocks in bits 10..19,
+  // deep ones in bits 0..9.
+  int nh = 0, nd = 0, nc = 0;
   bool wide = false;
 #pragma unroll
   for (int j = 0; j < kTailBlocksPerLane; ++j) {
-    nh += bm[j] >= t ? 1 : 0;
-    wide = wide || (bm[j] >= t && len[j] > kTailBlockKeys);
+    const bool deep = third[j] >= t;
+    nh += (uint32_t)(w0[j] >> 32) >= t ? 1 : 0;
+    nd += deep ? 1 : 0;
+    nc += !deep && (uint32_t)(w0[j] >> 32) >= t ? 1 : 0;
+    nc += !deep && (uint32_t)(w1[j] >> 32) >= t ? 1 : 0;
+    wide = wide || (deep && len[j] > kTailBlockKeys);
   }
-  const int incl = (int)wave_inclusive_scan((uint32_t)nh);
-  const int nhot = __builtin_amdgcn_readlane(incl, kWave - 1);  // >= 1
+  const uint32_t incl = wave_inclusive_scan(((uint32_t)nc << 20) | ((uint32_t)nh << 10) | (uint32_t)nd);
+  const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+  const int ndeep = (int)(tot & 0x3FFu), nhot = (int)((tot >> 10) & 0x3FFu);
   if (cap > 0 && nhot <= kTailHotMax && __ballot(wide) == 0) {
-    int o = incl - nh;
+    // Record keys >= T of the blocks that are not deep.
+    int ncand = (int)(tot >> 20);
+    {
+      int o = (int)(incl >> 20) - nc;
 #pragma unroll
-    for (int j = 0; j < kTailBlocksPerLane; ++j)
-      if (bm[j] >= t) hot[o++] = ((uint32_t)bs[j] << 8) | (uint32_t)len[j];
-    wave_sync_lds();
-    // Round trip 2: the keys of hot workgroup h go to lanes 8 (h % 8) ..
-    // 8 (h % 8) + 7, two each, in round h / 8 (registers x[2 (h / 8)] and
-    // x[2 (h / 8) + 1]; past a workgroup's count: out of range, key 0), so
-    // that each load instruction reads eight runs of 16 bytes; read again
-    // until every key carries the tag.
-    constexpr int kRounds = kTailBlockKeys / 2;
-    static_assert(kRounds * 8 >= kTailHotMax, "eight hot workgroups per round");
-    int start[kRounds], cnt[kRounds];
-    const int sub = 2 * (lane & 7);
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-      const int h = 8 * r + (lane >> 3);
-      const uint32_t hb = h < nhot ? (uint32_t)hot[h] : 0u;
-      start[r] = (int)(hb >> 8) + sub;
-      cnt[r] = (int)(hb & 255u) - sub;  // keys of this lane's pair inside the workgroup: min(2, cnt)
+      for (int j = 0; j < kTailBlocksPerLane; ++j) {
+        const bool shallow = third[j] < t;
+        if (shallow && (uint32_t)(w0[j] >> 32) >= t) cand[o++] = w0[j];
+        if (shallow && (uint32_t)(w1[j] >> 32) >= t) cand[o++] = w1[j];
+      }
     }
-    uint64_t x[kTailBlockKeys];
-    for (;;) {
-      bool stale = false;
+    if (ndeep > 0) {
+      int o = (int)(incl & 0x3FFu) - nd;
+#pragma unroll
+      for (int j = 0; j < kTailBlocksPerLane; ++j)
+        if (third[j] >= t) deep_list[o++] = ((uint32_t)bs[j] << 8) | (uint32_t)len[j];
+      wave_sync_lds();
+      // Round trip 2: eight lanes per deep block, two keys each (past the
+      // block's count: out of range, key 0), all rounds issued together,
+      // read until every key carries the tag.
+      constexpr int kRounds = (kTailHotMax + 7) / 8;
+      const int sub = 2 * (lane & 7);
+      int start[kRounds], cnt[kRounds];
 #pragma unroll
       for (int r = 0; r < kRounds; ++r) {
+        const int h = 8 * r + (lane >> 3);
+        const uint32_t hb = h < ndeep ? (uint32_t)deep_list[h] : 0u;
+        start[r] = (int)(hb >> 8) + sub;
+        cnt[r] = (int)(hb & 255u) - sub;
+      }
+      uint64_t x[2 * kRounds];
+      for (;;) {
+        uint32_t st = 0;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const bool in = e < cnt[r];
-          x[2 * r + e] = load_b64_coherent(rk, in ? (start[r] + e) * 8 : n * 8);
-          stale = stale || (in && ((uint32_t)x[2 * r + e] & kTailTagMask) != ktag);
+        for (int r = 0; r < kRounds; ++r) {
+          if (8 * r >= ndeep) break;
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            x[2 * r + e] = load_b64_coherent(rk, e < cnt[r] ? (start[r] + e) * 8 : n * 8);
+            st |= (uint32_t)(e < cnt[r]) & (uint32_t)!key_current(x[2 * r + e]);
+          }
         }
+        if (__ballot(st != 0) == 0) break;
+        if (expired()) {
+          give_up();
+          return;
+        }
+        __builtin_amdgcn_s_sleep(1);
       }
-      if (__ballot(stale) == 0) break;
-      if (expired()) {
-        give_up();
-        return;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    // Candidates: keys >= T (at least k of them).
-    int c2 = 0;
-    uint64_t y = 0;
 #pragma unroll
-    for (int q = 0; q < kTailBlockKeys; ++q) {
-      const bool take = (uint32_t)(x[q] >> 32) >= t;
-      c2 += take ? 1 : 0;
-      y = take ? x[q] : y;
-    }
-    if (__ballot(c2 > 1) == 0) {
-      // At most one candidate per lane: rank by readlane over the lanes
-      // holding one (full keys are distinct).
-      uint64_t m = __ballot(c2 == 1);
-      int r = 0;
-      while (m != 0) {
-        const int j = (int)__builtin_ctzll(m);
-        m &= m - 1;
-        r += readlane_u64(y, j) > y ? 1 : 0;
+      for (int r = 0; r < kRounds; ++r) {
+        if (8 * r >= ndeep) break;
+        const uint64_t x0 = x[2 * r], x1 = x[2 * r + 1];
+        const bool c0 = (uint32_t)(x0 >> 32) >= t, c1 = (uint32_t)(x1 >> 32) >= t;
+        const uint64_t m0 = __ballot(c0), m1 = __ballot(c1);
+        if (c0) cand[ncand + rank_below(m0)] = x0;
+        if (c1) cand[ncand + __popcll(m0) + rank_below(m1)] = x1;
+        ncand += __popcll(m0) + __popcll(m1);
       }
-      if (c2 == 1 && r < k) tail_write(y, out_s + r, out_i + r);
-      wave_sync_lds();
-      return;
     }
-    const int incl2 = (int)wave_inclusive_scan((uint32_t)c2);
-    const int total = __builtin_amdgcn_readlane(incl2, kWave - 1);  // >= k
-    int o2 = incl2 - c2;
-#pragma unroll
-    for (int q = 0; q < kTailBlockKeys; ++q)
-      if ((uint32_t)(x[q] >> 32) >= t) cand[o2++] = x[q];
+    // Rank of each candidate: the candidates above it (distinct full keys),
+    // counted over the list eight at a time (zero keys pad it).
+    if (lane < 8) cand[ncand + lane] = 0ull;
     wave_sync_lds();
-    for (int s = lane; s < total; s += kWave) {
-      const uint64_t z = cand[s];
+    for (int i0 = 0; i0 < ncand; i0 += kWave) {
+      const int i = i0 + lane;
+      const uint64_t y = i < ncand ? (uint64_t)cand[i] : ~0ull;
       int r = 0;
-      for (int q = 0; q < total; ++q) r += cand[q] > z ? 1 : 0;
-      if (r < k) tail_write(z, out_s + r, out_i + r);
+      for (int j = 0; j < ncand; j += 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r += (uint64_t)cand[j + e] > y ? 1 : 0;
+      }
+      if (i < ncand && r < k) tail_write(y, out_s + r, out_i + r);
     }
     wave_sync_lds();
     return;
