@@ -47,13 +47,21 @@ int msim_abi_version(void);
 int msim_set_docs_per_wave(int value);
 int msim_get_docs_per_wave(void);
 /* Top-k selection of the int8-query search: 1 (default) = the scan's
- * last workgroup selects when the call fits (k <= 32, 256..4096 documents,
- * <= 8 batch rows per scan pass), 0 = always a separate selection launch,
- * 2 = fused with the selection's k-round path forced (tests both paths).
+ * workgroup 0 selects, once the other workgroups' results have arrived, when
+ * the call fits (k <= 32, 256..4096 documents, <= 8 batch rows per scan
+ * pass), 0 = always a separate selection launch, 2 = fused with the
+ * selection's k-round path forced (tests both paths).
  * No counterpart in the reference, which selects on the host
  * (cuda_extension.cu:1629-1692 returns full score rows). */
 int msim_set_fused_topk(int mode);
 int msim_get_fused_topk(void);
+/* Prefix (sign) pass of the binary-prefix + int4-residual cascade
+ * (msim_binary_cascade_topk*): 1 (default) = the int8-query scan kernel
+ * over the sign stream when it applies (query rows of <= 128 tokens, token
+ * scales in [2^-122, 2^109)), 0 = the generalized scorer (tests both).  No
+ * counterpart in the reference, which has no such format. */
+int msim_set_prefix_scan(int mode);
+int msim_get_prefix_scan(void);
 /* Work split of the int8-query scan: 0 (default) = documents to waves
  * longest first, each to the least-loaded wave (whole corpus addressed from
  * one base; up to 2^25 tokens and 2^24 documents, beyond that as 1);

@@ -72,14 +72,25 @@ def get_docs_per_wave() -> int:
 
 
 def set_fused_topk(mode: int) -> None:
-    """Top-k selection of the int8-query search: 1 = in the scan's last
-    workgroup when the call fits (default), 0 = separate launch, 2 = fused
-    with the k-round selection path forced (testing)."""
+    """Top-k selection of the int8-query search: 1 = in the scan's workgroup 0
+    when the call fits (default), 0 = separate launch, 2 = fused with the
+    k-round selection path forced (testing)."""
     check(_native.load().msim_set_fused_topk(int(mode)))
 
 
 def get_fused_topk() -> int:
     return int(_native.load().msim_get_fused_topk())
+
+
+def set_prefix_scan(mode: int) -> None:
+    """Prefix pass of binary-prefix + int4-residual cascades: 1 = the int8-query
+    scan kernel over the sign stream when it applies (default), 0 = the
+    generalized scorer (testing)."""
+    check(_native.load().msim_set_prefix_scan(int(mode)))
+
+
+def get_prefix_scan() -> int:
+    return int(_native.load().msim_get_prefix_scan())
 
 
 def set_scan_partition(mode: int) -> None:

@@ -32,6 +32,8 @@ SIGNATURES: dict[str, list] = {
     "msim_get_fused_topk": [],
     "msim_set_scan_partition": [c_int],
     "msim_get_scan_partition": [],
+    "msim_set_prefix_scan": [c_int],
+    "msim_get_prefix_scan": [],
     # int4 handle
     "msim_int4_create": [c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_dbl, c_vp],
     "msim_int4_destroy": [c_vp],

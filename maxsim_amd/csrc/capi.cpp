@@ -16,6 +16,7 @@ thread_local std::string g_last_error;
 int g_docs_per_wave = 0;
 int g_fused_topk = 1;  // msim_set_fused_topk
 int g_scan_partition = 0;  // msim_set_scan_partition
+int g_scan_prefix = 1;     // msim_set_prefix_scan
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -109,6 +110,15 @@ extern "C" int msim_set_scan_partition(int mode) {
 }
 
 extern "C" int msim_get_scan_partition(void) { return g_scan_partition; }
+
+extern "C" int msim_set_prefix_scan(int mode) {
+  return guarded([&] {
+    if (mode < 0 || mode > 1) throw InvalidArgument("prefix scan mode must be 0 or 1");
+    g_scan_prefix = mode;
+  });
+}
+
+extern "C" int msim_get_prefix_scan(void) { return g_scan_prefix; }
 
 // -------------------------------------------------------------- int4 handle
 

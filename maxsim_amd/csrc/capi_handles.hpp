@@ -143,6 +143,12 @@ struct msim_binary_docs {
   double residual_scale = 1.0;
   int64_t max_doc_tiles = 1;  // 16-token tiles of the longest document
   msim::DeviceBuffer residual_packed, residual_token_scales16;
+  // The int8-query scan over the sign stream (a cascade's prefix pass): its
+  // tables (cached by wave count) and whether every token scale suits its
+  // one-fma epilogue ([kScanFmaMinScale, kScanFmaMaxScale)).
+  bool token_scales_fma = false;
+  int64_t scan_partition_waves = 0, num_scan_waves = 0, scan_tile_stride = 0;
+  msim::DeviceBuffer scan_wave_info, scan_tile_table;
   msim::DeviceBuffer scores, top_scores, top_indices, iscores;
   msim::ScoreWorkspace ws;
 
@@ -151,7 +157,8 @@ struct msim_binary_docs {
            residual_token_scales16.cap;
   }
   uint64_t workspace_bytes() const {
-    return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + ws.bytes();
+    return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + scan_wave_info.cap +
+           scan_tile_table.cap + ws.bytes();
   }
 };
 

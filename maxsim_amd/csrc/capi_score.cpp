@@ -530,6 +530,8 @@ extern "C" int msim_binary_set_token_scale(msim_binary_docs* h, const float* tok
     std::vector<float> v(token_scales, token_scales + count);
     upload_vec(h->token_scales, v, "copy binary token scale vector to device");
     h->has_token_scale = true;
+    h->token_scales_fma = true;
+    for (float x : v) h->token_scales_fma = h->token_scales_fma && x >= kScanFmaMinScale && x < kScanFmaMaxScale;
   });
 }
 
@@ -862,6 +864,65 @@ DocStreams binres_streams(msim_binary_docs* h, bool fused) {
   return s;
 }
 
+// The prefix (sign) pass of a cascade on the int8-query scan kernel: the
+// query rows are quantised once (the sign layout for this pass, the int4
+// layout for the rescoring pass, which reads them back with from_alt), then
+// score[b, n] = sum_q sigma_q max_t a_t (q8 . sign_t) in numpy's pairwise
+// float64 order -- the prefix scores of the host format, bit for bit.  False
+// (nothing done) when the scan does not apply: query rows of more than 128
+// tokens, or token scales outside the one-fma epilogue's range.
+bool binres_scan_prefix(msim_binary_docs* h, const float* d_query, int64_t batch, int64_t query_tokens, float* d_out,
+                        hipStream_t stream) {
+  if (!h->token_scales_fma || query_tokens <= 0 || query_tokens > kScanPassRows || h->num_docs == 0 ||
+      h->num_tokens == 0)
+    return false;
+  const int64_t waves = std::max<int64_t>(1, std::min<int64_t>((int64_t)device_cu_count() * kScanWavesPerCu, h->num_docs));
+  if (h->scan_partition_waves != waves) {
+    std::vector<int64_t> info;
+    std::vector<uint64_t> tiles;
+    build_scan_tables(h->host_offsets.data(), h->num_docs, waves, false, info, tiles, h->scan_tile_stride,
+                      h->num_scan_waves);
+    upload_vec(h->scan_wave_info, info, "copy sign scan wave table to device");
+    upload_vec(h->scan_tile_table, tiles, "copy sign scan tile table to device");
+    h->scan_partition_waves = waves;
+  }
+  ScoreWorkspace& ws = h->ws;
+  const int64_t rows = batch * query_tokens, rows_padded = ceil_div(rows, 16) * 16 + 128;
+  ws.qpack.ensure((size_t)rows_padded * 128, "hipMalloc query limbs");
+  ws.qpack_alt.ensure((size_t)rows_padded * 128, "hipMalloc query limbs (int4 layout)");
+  ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
+  ws.qsum.ensure(sizeof(int32_t) * rows_padded, "hipMalloc query limb sums");
+  check_hip(launch_quantize_limbs(d_query, rows, rows_padded, 1, kDocSign, false, ws.qpack.as<int8_t>(),
+                                  ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream, kDocInt4,
+                                  ws.qpack_alt.as<int8_t>()),
+            "launch query quantize kernel");
+  ScanArgs a{};
+  a.codes = h->packed.as<uint8_t>();
+  a.token_scale16 = h->token_scales.as<float>();
+  a.offsets = h->offsets.as<int64_t>();
+  a.wave_info = h->scan_wave_info.as<int64_t>();
+  a.tile_table = h->scan_tile_table.as<uint64_t>();
+  a.tile_stride = h->scan_tile_stride;
+  a.num_waves = h->num_scan_waves;
+  a.q_row_order = 1;
+  a.doc_sign = 1;
+  a.query_tokens = (int32_t)query_tokens;
+  a.scale = 1.0;
+  a.score_stride = h->num_docs;
+  a.num_docs = h->num_docs;
+  const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
+  for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
+    const int64_t nb = std::min(per_pass, batch - b0), row0 = b0 * query_tokens;
+    a.qpack = ws.qpack.as<int8_t>() + row0 * 128;
+    a.qscale = ws.colmul.as<float>() + row0;
+    a.qsum = ws.qsum.as<int32_t>() + row0;
+    a.batch = (int32_t)nb;
+    a.scores = d_out + b0 * h->num_docs;
+    check_hip(launch_int8q_scan(a, kScanEpiFma, stream), "launch int8q sign scan kernel");
+  }
+  return true;
+}
+
 void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, int64_t query_tokens, int64_t k,
                     int64_t m, float* d_top_s, int64_t* d_top_i, hipStream_t stream) {
   const DocStreams prefix = binres_streams(h, false), fused = binres_streams(h, true);
@@ -887,6 +948,7 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
   cascade_device(
       h->ws, batch, h->num_docs, k, m,
       [&](float* d) {
+        if (g_scan_prefix && binres_scan_prefix(h, d_query, batch, query_tokens, d, stream)) return;
         run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, coarse_q, kRedMax, 1.0f, batch, query_tokens,
                           nullptr, Targets{}, d, h->num_docs, nullptr, stream);
       },
@@ -954,8 +1016,12 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
     qi.limbs = 1;
     Targets t{candidates, num_candidates, candidates != nullptr};
     h->scores.ensure(sizeof(float) * batch * targets, "hipMalloc score cache");
-    run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr, t,
-                      h->scores.as<float>(), targets, nullptr, nullptr);
+    // Prefix scores of every document: the scan a cascade's prefix pass uses.
+    const bool scanned = !fused && !candidates && g_scan_prefix &&
+                         binres_scan_prefix(h, qi.d_query, batch, query_tokens, h->scores.as<float>(), nullptr);
+    if (!scanned)
+      run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr, t,
+                        h->scores.as<float>(), targets, nullptr, nullptr);
     check_hip(hipMemcpy(out, h->scores.ptr, sizeof(float) * batch * targets, hipMemcpyDeviceToHost),
               "copy output to host");
   });

@@ -140,7 +140,7 @@ struct TileEpi {
 constexpr int kMagic = 0x4B000000;
 constexpr int kMaskedAcc = -(1 << 30);  // C operand of masked rows (|16 * dot| < 2^21)
 
-template <int NT, int EPI, bool kTail>
+template <int NT, int EPI, bool kTail, bool kSign = false>
 __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_kernel(
     ScanArgs p, const uint8_t* __restrict__ codes, const float* __restrict__ token_scale16,
     const int64_t* __restrict__ offsets, const int64_t* __restrict__ wave_info_ptr,
@@ -209,8 +209,13 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     const uint32_t q_lds = wave_uniform((int)lds_address(s_query));
 #pragma unroll
     for (int i = 0; i < kQueryParts; ++i) {
-      const uint32_t part = (uint32_t)((i * kScanWaves + wave) * kWave);
-      lds_load_b128(rqp, (part + (uint32_t)lane) * 16u, q_lds + part * 16u);
+      const uint32_t half = (uint32_t)(i * kScanWaves + wave), part = half * kWave;
+      // Lane order: the half-tile is one linear 1 KiB run.  Row order (128
+      // bytes per row): lane (g, c) takes row 16 (half / 2) + c, bytes
+      // 32g + 16 (half % 2) .. + 16.
+      const uint32_t src = p.q_row_order ? ((16u * (half >> 1) + (uint32_t)c) * 128u + 32u * (uint32_t)g + 16u * (half & 1u))
+                                         : (part + (uint32_t)lane) * 16u;
+      lds_load_b128(rqp, src, (uint32_t)wave_uniform((int)(q_lds + part * 16u)));
     }
     const v4i rq = make_rsrc_words(qscale, (uint32_t)(16 * NT * 4));
     const uint32_t qs_lds = wave_uniform((int)lds_address(qs));
@@ -219,11 +224,19 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     // Fused: the launch counter into lane 0's word of the row-maxima buffer
     // (the other lanes read past the 4-byte range: 0).
     if (fused) lds_load_b32(make_rsrc_words(p.epoch, 4u), 4u * (uint32_t)lane, wave_uniform((int)lds_address(rowmax)));
+    // Sign documents: the query rows' code sums into the row-maxima buffer.
+    if (kSign) {
+      const v4i rsum = make_rsrc_words(p.qsum, (uint32_t)(16 * NT * 4));
+      const uint32_t rm_lds = wave_uniform((int)lds_address(rowmax));
+      lds_load_b32(rsum, 4u * (uint32_t)lane, rm_lds);
+      lds_load_b32(rsum, 4u * (uint32_t)(lane + kWave), rm_lds + 4 * kWave);
+    }
   }
 
   // Bounds-checked descriptors over the wave's tokens (rows past the wave
   // read zero).
-  const v4i rc = make_rsrc_words(codes + T0 * 64, (uint32_t)((T1 - T0) * 64));
+  constexpr int kTokenBytes = kSign ? 16 : 64;
+  const v4i rc = make_rsrc_words(codes + T0 * kTokenBytes, (uint32_t)((T1 - T0) * kTokenBytes));
   const v4i rs = make_rsrc_words(kTS ? (const void*)(token_scale16 + T0) : (const void*)codes,
                                  kTS ? (uint32_t)((T1 - T0) * 4) : 0u);
   const uint32_t ring_codes = wave_uniform((int)lds_address(&s_codes[wave][0][0]));
@@ -239,7 +252,8 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   constexpr int kOps = kTS ? 2 : 1;
   constexpr int kRingWait = (kPrefetch - 1) * kOps;
   auto load_tile = [&](int slot_, uint32_t t) {
-    lds_load_b128(rc, (t + (uint32_t)c) * 64u + 16u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
+    if (kSign) lds_load_b32(rc, (t + (uint32_t)c) * 16u + 4u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
+    else lds_load_b128(rc, (t + (uint32_t)c) * 64u + 16u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
     if (kTS) lds_load_b32(rs, (t + (uint32_t)c) * 4u, ring_scales + slot_ * kWave * 4);
   };
 #pragma unroll
@@ -250,6 +264,17 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   vm_wait_lds<kPrefetch * kOps>();
   __builtin_amdgcn_s_barrier();
   if (fused) tag = (uint32_t)wave_uniform((int)__float_as_uint(rowmax[0])) + 1u;
+  // Sign documents (A bytes 0 / 2 from the sign bits): the first MFMA of
+  // query tile j starts at 2^23 - sum(q8) in column c, so the accumulator
+  // holds 2^23 + (2 (q8 . bits) - sum(q8)) = 2^23 + q8 . signs.
+  v4i csign[kSign ? NT : 1];
+  if (kSign) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int cj = kMagic - __float_as_int(rowmax[16 * j + c]);
+      csign[j] = (v4i){cj, cj, cj, cj};
+    }
+  }
   // Query tiles: lane (g, c) holds row 16j + c, dims of lane group g; half j
   // of tile h is the linear 1 KiB run 2j + h (no bank conflicts).
   v4i blo[NT], bhi[NT];
@@ -329,19 +354,30 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // halves' operand is unpacked beside the first four groups.
   auto issue_and_finish = [&](v4i (&acc_q)[NT], const v4u& w_q, const v4i& cinit, const v4i (&acc_p)[NT],
                               const TileEpi& e_p, bool with_epilogue) {
+    // int4: sixteen times the even / odd dims' values.  Sign documents (32
+    // bits, bit 8y + i = dim 32g + 8y + i): byte y of operand dword i is 2 x
+    // bit 8y + i (lo, i < 4) or bit 8y + i + 4 (hi).
+    auto unpack_lo = [&](int x) -> int {
+      if (kSign) return (int)((x == 0 ? (w_q[0] << 1) : (w_q[0] >> (x - 1))) & 0x02020202u);
+      return (int)((w_q[x] << 4) & 0xF0F0F0F0u);
+    };
+    auto unpack_hi = [&](int x) -> int {
+      if (kSign) return (int)((w_q[0] >> (x + 3)) & 0x02020202u);
+      return (int)(w_q[x] & 0xF0F0F0F0u);
+    };
     v4i lo, hi;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) lo[x] = (int)((w_q[x] << 4) & 0xF0F0F0F0u);
+    for (int x = 0; x < 4; ++x) lo[x] = unpack_lo(x);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      acc_q[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], cinit, 0, 0, 0);
+      acc_q[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], kSign ? csign[kSign ? j : 0] : cinit, 0, 0, 0);
       if (with_epilogue) epilogue_half(acc_p[j], e_p, j, 0);
-      if (j < 4) hi[j] = (int)(w_q[j] & 0xF0F0F0F0u);
+      if (j < 4) hi[j] = unpack_hi(j);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int x = NT; x < 4; ++x) hi[x] = (int)(w_q[x] & 0xF0F0F0F0u);
+    for (int x = NT; x < 4; ++x) hi[x] = unpack_hi(x);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       acc_q[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc_q[j], 0, 0, 0);
@@ -426,7 +462,11 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     uint64_t meta = tt[0], iss = tt[kPrefetch];
     int slot = 0;
     vm_wait_lds<kRingWait>();
-    v4u w = s_codes[wave][0][lane];
+    auto read_codes = [&](int sl) -> v4u {
+      if (kSign) return (v4u){reinterpret_cast<const uint32_t*>(&s_codes[wave][sl][0])[lane], 0u, 0u, 0u};
+      return s_codes[wave][sl][lane];
+    };
+    v4u w = read_codes(0);
     v4u sv = kTS ? *reinterpret_cast<const v4u*>(&s_scales[wave][0][0] + 4 * g) : (v4u){0u, 0u, 0u, 0u};
     // Read-ahead after tile `slot` left the ring for registers.
     auto advance = [&](int i_next) {
@@ -435,7 +475,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       const uint64_t meta_n = tt[i_next], iss_n = tt[i_next + kPrefetch];
       slot = slot + 1 == kPrefetch ? 0 : slot + 1;
       vm_wait_lds<kRingWait>();
-      w = s_codes[wave][slot][lane];
+      w = read_codes(slot);
       if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
       meta = meta_n;
       iss = iss_n;
@@ -534,14 +574,14 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (threadIdx.x == 0) __hip_atomic_store(p.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int EPI, bool kTail>
+template <int EPI, bool kTail, bool kSign>
 static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_t stream) {
   const dim3 grid((unsigned)blocks), block(kScanThreads);
   switch (nt) {
-#define MSIM_SCAN_CASE(N)                                                                           \
-  int8q_scan_kernel<N, EPI, kTail><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets,      \
-                                                        a.wave_info, a.tile_table, a.qpack, a.qscale, \
-                                                        a.scores)
+#define MSIM_SCAN_CASE(N)                                                                                   \
+  int8q_scan_kernel<N, EPI, kTail, kSign><<<grid, block, 0, stream>>>(a, a.codes, a.token_scale16, a.offsets, \
+                                                                      a.wave_info, a.tile_table, a.qpack,     \
+                                                                      a.qscale, a.scores)
     case 1: MSIM_SCAN_CASE(1); break;
     case 2: MSIM_SCAN_CASE(2); break;
     case 3: MSIM_SCAN_CASE(3); break;
@@ -556,8 +596,8 @@ static void launch_scan_nt(const ScanArgs& a, int nt, int64_t blocks, hipStream_
 
 template <int EPI>
 static void launch_scan_epi(const ScanArgs& a, int nt, int64_t blocks, bool tail, hipStream_t stream) {
-  if (tail) launch_scan_nt<EPI, true>(a, nt, blocks, stream);
-  else launch_scan_nt<EPI, false>(a, nt, blocks, stream);
+  if (tail) launch_scan_nt<EPI, true, false>(a, nt, blocks, stream);
+  else launch_scan_nt<EPI, false, false>(a, nt, blocks, stream);
 }
 
 hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t stream) {
@@ -566,6 +606,9 @@ hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t str
     return hipErrorInvalidValue;
   if (epilogue != kScanEpiIntMax && epilogue != kScanEpiFma && epilogue != kScanEpiCvt) return hipErrorInvalidValue;
   if ((epilogue == kScanEpiIntMax) != (args.token_scale16 == nullptr)) return hipErrorInvalidValue;
+  // Sign documents: the one-fma epilogue over the per-token scales, no fused
+  // selection, the query code sums given.
+  if (args.doc_sign && (epilogue != kScanEpiFma || args.topk_k > 0 || args.qsum == nullptr)) return hipErrorInvalidValue;
   if (args.topk_k > 0 &&
       (args.topk_k > kScanTailMaxK || args.topk_k > args.num_docs || args.num_docs > kScanTailMaxDocs ||
        args.num_docs < kScanTailMinDocs || args.batch > kScanTailMaxRows ||
@@ -576,6 +619,10 @@ hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t str
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;
   const bool tail = args.topk_k > 0;
+  if (args.doc_sign) {
+    launch_scan_nt<kScanEpiFma, false, true>(args, nt, blocks, stream);
+    return hipGetLastError();
+  }
   switch (epilogue) {
     case kScanEpiIntMax: launch_scan_epi<kScanEpiIntMax>(args, nt, blocks, tail, stream); break;
     case kScanEpiFma: launch_scan_epi<kScanEpiFma>(args, nt, blocks, tail, stream); break;

@@ -83,6 +83,11 @@ struct ScanArgs {
   int64_t tile_stride;
   int64_t num_waves;            // a multiple of kScanWavesPerGroup
   const int8_t* qpack;          // >= rows + 128 rows of MFMA B-order int8 codes (zero past rows)
+  int32_t q_row_order;          // qpack rows of 128 bytes (quantize_limbs) instead of the scan's lane order
+  int32_t doc_sign;             // sign documents: codes 16 bytes per token (32 sign bits per lane group,
+                                //   bit b = dim 32g + b), token_scale16 the per-token scales themselves,
+                                //   qpack in the sign layout of quantize_limbs
+  const int32_t* qsum;          // sign documents: per query row the sum of its int8 codes
   const float* qscale;          // per-row query scale, same row count
   int32_t batch;                // batch rows of this pass (batch * query_tokens <= 128)
   int32_t query_tokens;

@@ -115,9 +115,39 @@ def test_binres_scores_match_oracle(gpu, oracle):
            oracle.binres_fused_scores(query, signs, a, rv, rs, offsets, candidates=cand), 1e-6)
 
 
-def test_binres_cascade_equals_host_procedure(gpu):
+@pytest.fixture
+def prefix_scan():
+    from maxsim_amd import _maxsim_hip
+
+    yield _maxsim_hip.set_prefix_scan
+    _maxsim_hip.set_prefix_scan(1)
+
+
+@pytest.mark.parametrize("shape", [(3, 9), (4, 32), (2, 64), (1, 5), (8, 16)])
+def test_binres_prefix_scan_is_bit_exact(gpu, oracle, prefix_scan, shape):
+    """The prefix pass on the int8-query scan (sign documents: A bytes 0 / 2,
+    the query sums in the MFMA's C operand) equals the oracle's prefix scores
+    bit for bit; the generalized scorer agrees to rtol 1e-6."""
+    from maxsim_amd.binres import binres_score
+
+    docs, offsets = ragged_fixture(220, 53, lo=1, hi=90)  # short (< 16), long and one empty document
+    batch, qt = shape
+    query = np.random.default_rng(54 + qt).standard_normal((batch, qt, 128)).astype(np.float32)
+    packed = _binres(docs, offsets)
+    signs, a, _, _, _ = oracle.pack_binary_residual(docs)
+    exp = oracle.binres_prefix_scores(query, signs, a, offsets)
+    prefix_scan(1)
+    np.testing.assert_array_equal(binres_score(query, packed, fused=False), exp)
+    prefix_scan(0)
+    _close(binres_score(query, packed, fused=False), exp, 1e-6)
+
+
+@pytest.mark.parametrize("mode", [1, 0])
+def test_binres_cascade_equals_host_procedure(gpu, prefix_scan, mode):
     from maxsim_amd import synthetic
     from maxsim_amd.binres import binres_cascade_topk, binres_score
+
+    prefix_scan(mode)
 
     corpus = synthetic.make_corpus(400, 64, 192, seed=47)
     query = synthetic.make_queries(corpus, 4)
