@@ -38,7 +38,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-SCAN_KERNEL = "int8q_scan_kernel<8, 1, true>"  # the scan (one-fma epilogue) with its fused top-k tail
+SCAN_KERNEL = "int8q_scan_kernel<8, 1, true, false>"  # the scan (one-fma epilogue, int4 documents) with its fused top-k tail
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "int8q_scan_config2_traffic.md")
 CALIBRATION_BYTES = 256 << 20  # one plain copy: reads and writes this many bytes
 SCAN_BLOCK = 10  # scan launches between two events
@@ -66,16 +66,20 @@ def parse_args():
     return ap.parse_args()
 
 
-def algorithmic_bytes(num_tokens: int, num_docs: int, batch: int, query_tokens: int, k: int) -> dict:
+def algorithmic_bytes(num_tokens: int, num_docs: int, batch: int, query_tokens: int, k: int,
+                      num_blocks: int = 512) -> dict:
     """Bytes the scan kernel (with its fused top-k) must move per launch over a
     per-token int4 corpus: 64 B of int4 codes + 4 B token scale per token, 8 B
     per document offset, the quantised query (128 B codes + 4 B scale per
-    query row, read once per workgroup from L2 but counted once), the f32
-    score of every (batch row, document) written once and read once by the
-    selection, and the top-k (4 B score + 8 B id each)."""
+    query row, read once per workgroup from L2 but counted once), the 8-byte
+    selection key of every (batch row, document) written once, each
+    workgroup's 24-byte record per batch row written once and read once by the
+    selecting workgroup, and the top-k (4 B score + 8 B id each).  The
+    selection also reads back the keys of a few workgroups (those holding a
+    key at or above its threshold); they are not counted."""
     corpus = 68 * num_tokens + 8 * (num_docs + 1)
     query = batch * query_tokens * (128 + 4)
-    out = 2 * 4 * batch * num_docs + 12 * batch * k
+    out = 8 * batch * num_docs + 2 * 24 * batch * num_blocks + 12 * batch * k
     return {"corpus": corpus, "query": query, "out": out, "total": corpus + query + out}
 
 
@@ -306,7 +310,9 @@ def bench_config2(args):
         handle._h, batch, qtok, ptr(scores), sptr)))
     assert np.array_equal(scores.cpu().numpy(), ref_scores), "scan scores differ between entry points"
 
-    nbytes = algorithmic_bytes(num_tokens, num_docs, batch, qtok, k)
+    # the scan's workgroups: eight waves per CU (four per workgroup), at most one wave per document
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nbytes = algorithmic_bytes(num_tokens, num_docs, batch, qtok, k, -(-min(cus * 8, num_docs) // 4))
     scan_avg_s = float(scan_ms.mean()) * 1e-3
     achieved = nbytes["total"] / scan_avg_s / 1e9
 
