@@ -116,22 +116,32 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   ScoreArgs a{};
   const int64_t* d_targets = nullptr;
   if (t.device) {
-    // Candidate lists on the device: fixed-size target ranges per wave,
-    // tables written by candidate_tables_kernel (or already by the selector).
+    // Candidate lists on the device: fixed-size target ranges per wave; with
+    // more than one per wave, tables written by candidate_tables_kernel (or
+    // already by the selector).
     if (!t.per_row) throw InvalidArgument("device candidate lists must be per batch row");
     const CandidateLayout cl = candidate_layout(batch, query_tokens, limbs, per_target, t.max_doc_tiles);
     const int64_t w4 = cl.waves;
-    ws.cand_info.ensure(sizeof(int64_t) * groups * w4 * kScoreInfoWords, "hipMalloc candidate wave table");
-    ws.cand_tiles.ensure(sizeof(uint64_t) * groups * w4 * cl.cap, "hipMalloc candidate tile table");
-    if (!t.tables_ready)
-      check_hip(launch_candidate_tables(t.device, per_target, groups, t.d_offsets, w4, cl.per_wave, cl.cap,
-                                        ws.cand_info.as<int64_t>(), ws.cand_tiles.as<uint64_t>(), stream),
-                "launch candidate table kernel");
-    a.wave_info = ws.cand_info.as<int64_t>();
-    a.tiles = ws.cand_tiles.as<uint64_t>();
-    a.num_waves = w4;
-    a.info_grp_stride = w4 * kScoreInfoWords;
     d_targets = t.device;
+    if (cl.per_wave == 1) {
+      // One candidate per wave: the kernel takes its tiles from the
+      // document's token range (no tables).
+      if (t.d_offsets == nullptr) throw InvalidArgument("device candidate lists need the token offsets");
+      a.direct_offsets = t.d_offsets;
+      a.direct_count = per_target;
+      a.num_waves = w4;
+    } else {
+      ws.cand_info.ensure(sizeof(int64_t) * groups * w4 * kScoreInfoWords, "hipMalloc candidate wave table");
+      ws.cand_tiles.ensure(sizeof(uint64_t) * groups * w4 * cl.cap, "hipMalloc candidate tile table");
+      if (!t.tables_ready)
+        check_hip(launch_candidate_tables(t.device, per_target, groups, t.d_offsets, w4, cl.per_wave, cl.cap,
+                                          ws.cand_info.as<int64_t>(), ws.cand_tiles.as<uint64_t>(), stream),
+                  "launch candidate table kernel");
+      a.wave_info = ws.cand_info.as<int64_t>();
+      a.tiles = ws.cand_tiles.as<uint64_t>();
+      a.num_waves = w4;
+      a.info_grp_stride = w4 * kScoreInfoWords;
+    }
   } else if (!t.host) {
     if (ws.full_key != waves) {
       std::vector<int64_t> info;
@@ -735,9 +745,10 @@ void check_cascade(int64_t k, int64_t m, int64_t num_docs) {
 // (score desc, document asc), put in document order -> fine scores of the
 // candidates -> top-k, ties by document id (cascade.py:294-453), all on the
 // device.  coarse(d_scores) and fine(d_candidate_ids, d_scores,
-// tables_ready) enqueue the two scoring passes; `layout` (the rescoring
-// pass's candidate_layout) lets the selector write the rescoring tables
-// itself, one launch fewer (tables_ready is then true).
+// tables_ready) enqueue the two scoring passes.  With one candidate per
+// rescoring wave (`layout`, the rescoring pass's candidate_layout) the pass
+// needs no tables; with more, the selector writes them itself, one launch
+// fewer (tables_ready is then true).
 template <typename Coarse, typename Fine>
 void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t k, int64_t m, Coarse coarse,
                     Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream, const CandidateLayout& layout,
@@ -747,19 +758,24 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
   ws.top_m_ids.ensure(sizeof(int64_t) * batch * m, "hipMalloc cascade candidates");
   bool tables_ready = false;
   if (num_docs <= kSortMaxRow) {
-    ws.cand_info.ensure(sizeof(int64_t) * batch * layout.waves * kScoreInfoWords, "hipMalloc candidate wave table");
-    ws.cand_tiles.ensure(sizeof(uint64_t) * batch * layout.waves * layout.cap, "hipMalloc candidate tile table");
+    // One candidate per rescoring wave needs no tables (the pass reads each
+    // candidate's token range itself).
+    const bool tables = layout.per_wave > 1;
     CandidateTables tab;
-    tab.d_offsets = d_offsets;
-    tab.waves = layout.waves;
-    tab.per_wave = layout.per_wave;
-    tab.cap = layout.cap;
-    tab.d_info = ws.cand_info.as<int64_t>();
-    tab.d_tiles = ws.cand_tiles.as<uint64_t>();
+    if (tables) {
+      ws.cand_info.ensure(sizeof(int64_t) * batch * layout.waves * kScoreInfoWords, "hipMalloc candidate wave table");
+      ws.cand_tiles.ensure(sizeof(uint64_t) * batch * layout.waves * layout.cap, "hipMalloc candidate tile table");
+      tab.d_offsets = d_offsets;
+      tab.waves = layout.waves;
+      tab.per_wave = layout.per_wave;
+      tab.cap = layout.cap;
+      tab.d_info = ws.cand_info.as<int64_t>();
+      tab.d_tiles = ws.cand_tiles.as<uint64_t>();
+    }
     check_hip(launch_select_topm(ws.coarse.as<float>(), batch, num_docs, num_docs, m, ws.top_m_ids.as<int64_t>(),
-                                 stream, &tab),
+                                 stream, tables ? &tab : nullptr),
               "launch cascade candidate selection");
-    tables_ready = true;
+    tables_ready = tables;
   } else {
     ws.top_m_scores.ensure(sizeof(float) * batch * m, "hipMalloc cascade candidate scores");
     check_hip(launch_topk(ws.coarse.as<float>(), batch, num_docs, num_docs, m, nullptr, ws.top_m_scores.as<float>(),

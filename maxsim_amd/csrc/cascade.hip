@@ -16,13 +16,12 @@ __device__ __forceinline__ uint64_t tile_entry(int64_t start, int64_t rows, bool
 }
 
 // Tables of wave w of group g: its candidates [t0, t0 + n) of the group's m
-// (n <= per_wave; cand(i) gives the group's i-th document), their tiles at
-// tiles[(g * waves + w) * cap ...]; the host sizes cap as per_wave *
-// (largest document's tile count) + 1.
-template <typename Cand>
-__device__ void candidate_wave_tables(Cand cand, int64_t m, int64_t g, const int64_t* __restrict__ offsets,
-                                      int64_t waves, int64_t w, int64_t per_wave, int64_t cap,
-                                      int64_t* __restrict__ info, uint64_t* __restrict__ tiles) {
+// (n <= per_wave; range(i) gives the token range [start, end) of the group's
+// i-th document), their tiles at tiles[(g * waves + w) * cap ...]; the host
+// sizes cap as per_wave * (largest document's tile count) + 1.
+template <typename Range>
+__device__ void candidate_wave_tables(Range range, int64_t m, int64_t g, int64_t waves, int64_t w, int64_t per_wave,
+                                      int64_t cap, int64_t* __restrict__ info, uint64_t* __restrict__ tiles) {
   const int64_t id = g * waves + w;
   const int64_t t0 = min(w * per_wave, m);
   const int64_t n = min(per_wave, m - t0);
@@ -30,8 +29,8 @@ __device__ void candidate_wave_tables(Cand cand, int64_t m, int64_t g, const int
   uint64_t* out = tiles + tab0;
   int64_t k = 0;
   for (int64_t i = 0; i < n; ++i) {
-    const int64_t doc = cand(t0 + i);
-    const int64_t s = offsets[doc], e = offsets[doc + 1];
+    int64_t s, e;
+    range(t0 + i, s, e);
     if (s == e) {
       out[k++] = tile_entry(0, 1, true, true, i);
       continue;
@@ -55,8 +54,13 @@ __global__ __launch_bounds__(256) void candidate_tables_kernel(const int64_t* __
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= groups * waves) return;
   const int64_t g = id / waves;
-  candidate_wave_tables([&](int64_t i) { return cands[g * m + i]; }, m, g, offsets, waves, id % waves, per_wave, cap,
-                        info, tiles);
+  candidate_wave_tables(
+      [&](int64_t i, int64_t& b, int64_t& e) {
+        const int64_t doc = cands[g * m + i];
+        b = offsets[doc];
+        e = offsets[doc + 1];
+      },
+      m, g, waves, id % waves, per_wave, cap, info, tiles);
 }
 
 // Ascending bitonic sort of s[0, pow2) in LDS by the whole block.
@@ -90,158 +94,175 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(int64_t* __restrict__ r
   for (int64_t i = threadIdx.x; i < n; i += blockDim.x) row[i] = s[i];
 }
 
-// Block-wide exclusive prefix sum of one value per thread (1024 threads):
-// wave scans by shuffles, then the wave totals.
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  uint32_t x = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t y = __shfl_up(x, d);
-    if (lane >= d) x += y;
-  }
-  if (lane == kWave - 1) s_wave[wave] = x;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
-    const uint32_t t = s_wave[w];
-    before += w < wave ? t : 0u;
-    all += t;
-  }
-  __syncthreads();
-  total = all;
-  return before + x - v;
+// Sum over each row of 16 lanes, in every lane of the row (DPP quad
+// butterflies, then rotations by 4 and 8).
+__device__ __forceinline__ uint32_t row_sum16(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true);  // row_ror:4
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true);  // row_ror:8
+  return v;
 }
 
 // Per row of n <= 4096 scores: the m best by (score desc, position asc)
 // (the order of _stable_topk, cascade.py:420-453), written as positions in
-// ascending order.  Radix selection of the m-th largest order-preserving
-// score key, 8 bits per round, then a stable compaction: keys above it, and
-// the first `need` keys equal to it in position order.
+// ascending order.  Keys are 44 bits, the order-preserving score key above
+// 4095 - position: distinct, and larger for a better element.  Radix
+// selection of the m-th largest key, 11 bits per round, starting below the
+// bits every key of the row shares (scores of one query lie in a narrow
+// range, so their top bits agree, and a digit over them would put every key
+// in one bin).  A round's histogram counts reversed digits (2047 - digit) in
+// 64 groups of 32 (one atomic per key; a pad word after each group keeps
+// reads across groups free of bank conflicts); after a barrier each wave
+// sums four groups, and after a second one every wave finds the digit itself
+// from two wave scans: the group where the running count reaches `need`,
+// then the digit inside it.  The rounds stop once the digit's count is what is still needed
+// (distinct keys guarantee it once every bit is fixed); the selected keys are
+// then those whose fixed bits are at least the prefix.  Positions are
+// written in ascending order from ballot counts per (slot, wave), one scan
+// over their 64 counts; with tables requested, the selected documents' token
+// ranges (loaded with the scores) stay in LDS for the rescoring pass's
+// tables.
 __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restrict__ scores, int64_t n,
                                                            int64_t stride, int64_t m, int64_t* __restrict__ out,
                                                            CandidateTables tab) {
-  constexpr int E = kSortMaxRow / 1024;  // positions 4 t .. 4 t + 3 of thread t
-  __shared__ uint32_t s_hist[4][256];
-  __shared__ uint32_t s_sel[kSortMaxRow];  // the selected positions, for the tables
-  __shared__ uint32_t s_wave[16];
-  __shared__ uint32_t s_or[16], s_and[16];
-  const int tid = threadIdx.x, lane = tid % kWave;
-  const float* row = scores + (int64_t)blockIdx.x * stride;
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
-  uint32_t key[E];
-  bool valid[E];
+  constexpr int kThreads = 1024, kWaves = kThreads / kWave;
+  constexpr int E = kSortMaxRow / kThreads;  // positions e * 1024 + t of thread t
+  constexpr int kBits = 11, kBins = 1 << kBits, kGroupBins = kBins / kWave, kRounds = 4;
+  constexpr int kGroupStride = kGroupBins + 1;  // one pad word per group: conflict-free reads across groups
+  static_assert(E * kWaves == kWave, "one lane per (slot, wave) count");
+  static_assert(kRounds * kBits >= 44 && kGroupBins == 32 && 4 * kWaves == kWave, "44-bit keys, 64 groups of 32");
+  __shared__ uint32_t s_hist[kRounds][kWave * kGroupStride];
+  __shared__ uint32_t s_group[kRounds][kWave];
+  __shared__ uint32_t s_or[kWaves], s_and[kWaves];
+  __shared__ uint32_t s_cnt[E * kWaves];
+  __shared__ int64_t s_beg[kSortMaxRow];
+  __shared__ uint32_t s_len[kSortMaxRow];
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const bool tables = tab.d_info != nullptr;
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(scores + (int64_t)blockIdx.x * stride, (uint32_t)(n * 4));
+  const __amdgpu_buffer_rsrc_t roff = make_rsrc(tables ? tab.d_offsets : nullptr, tables ? (uint32_t)((n + 1) * 8) : 0u);
+  uint32_t v[E];
+  int64_t beg[E], end[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int i = E * tid + e;
-    valid[e] = i < n;
-    key[e] = score_key(__uint_as_float(load_b32(rsrc, i * 4)));
+  for (int e = 0; e < E; ++e) v[e] = load_b32(rsrc, (e * kThreads + tid) * 4);
+  if (tables) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      beg[e] = (int64_t)load_b64(roff, (e * kThreads + tid) * 8);
+      end[e] = (int64_t)load_b64(roff, (e * kThreads + tid + 1) * 8);
+    }
   }
-  // The bits every key of the row shares are fixed first: scores of one
-  // query lie in a narrow range, so their top bits agree, and a radix digit
-  // over them would send every key to one histogram bin (serialised LDS
-  // atomics).  The rounds then take 8 bits at a time from the highest bit
-  // that varies.
+  for (int i = tid; i < kRounds * kWave * kGroupStride; i += kThreads) (&s_hist[0][0])[i] = 0u;
+  if (tid < kRounds * kWave) (&s_group[0][0])[tid] = 0u;
+  uint64_t key[E];
+  bool valid[E];
   uint32_t kor = 0u, kand = ~0u;
 #pragma unroll
-  for (int e = 0; e < E; ++e)
+  for (int e = 0; e < E; ++e) {
+    const int p = e * kThreads + tid;
+    const uint32_t sk = score_key(__uint_as_float(v[e]));
+    valid[e] = p < n;
+    key[e] = ((uint64_t)sk << 12) | (uint32_t)(kSortMaxRow - 1 - p);
     if (valid[e]) {
-      kor |= key[e];
-      kand &= key[e];
+      kor |= sk;
+      kand &= sk;
     }
-  for (int i = tid; i < 4 * 256; i += blockDim.x) (&s_hist[0][0])[i] = 0u;
+  }
   kor = wave_reduce(kor, [](uint32_t a, uint32_t b) { return a | b; });
   kand = wave_reduce(kand, [](uint32_t a, uint32_t b) { return a & b; });
   if (lane == 0) {
-    s_or[tid / kWave] = kor;
-    s_and[tid / kWave] = kand;
+    s_or[wave] = kor;
+    s_and[wave] = kand;
   }
   __syncthreads();
   kor = 0u;
   kand = ~0u;
-  for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
     kor |= s_or[w];
     kand &= s_and[w];
   }
   const uint32_t diff = kor ^ kand;
-  const int top = diff == 0u ? -1 : 31 - __clz(diff);  // highest varying bit
-  uint32_t mask = top >= 31 ? 0u : ~0u << (top + 1);
-  uint32_t prefix = kand & mask, need = (uint32_t)m;
-  // One histogram per round (at most four rounds of 8 bits), all zeroed
-  // before the reduction's barrier above, and every wave finds the digit
-  // itself from the histogram: one barrier per round.
-  int round = 0;
-  for (int hi = top; hi >= 0; hi -= 8, ++round) {
-    const int shift = hi >= 7 ? hi - 7 : 0;
-    const uint32_t dmask = (hi - shift == 31 ? ~0u : (2u << (hi - shift)) - 1u);  // digit of bits shift..hi
-    uint32_t* hist = s_hist[round];
+  const int top = diff != 0u ? 12 + (31 - __clz(diff)) : 11;  // highest bit in which keys may differ
+  constexpr uint64_t kKeyMask = (1ull << 44) - 1ull;
+  uint64_t mask = (~0ull << (top + 1)) & kKeyMask;
+  uint64_t prefix = ((uint64_t)kand << 12) & mask;
+  uint32_t need = (uint32_t)m;
+  if (m < n) {
+    for (int r = 0, hi = top;; ++r, hi -= kBits) {
+      const int shift = hi >= kBits - 1 ? hi - (kBits - 1) : 0;
+      const uint32_t dbits = (2u << (hi - shift)) - 1u;
+      uint32_t* hist = s_hist[r];
+      uint32_t* grp = s_group[r];
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-      if (valid[e] && (key[e] & mask) == prefix) atomicAdd(&hist[(key[e] >> shift) & dmask], 1u);
-    __syncthreads();
-    // Lane l holds digits 4l .. 4l + 3; suffix sums over the lanes from the
-    // top digit down find the digit where the count reaches `need` (exactly
-    // one lane finds it).
-    uint32_t c[4], local = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      c[j] = hist[4 * lane + j];
-      local += c[j];
-    }
-    uint32_t suffix = local;  // inclusive: lanes >= this one
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const uint32_t y = __shfl_down(suffix, d);
-      if (lane + d < kWave) suffix += y;
-    }
-    uint32_t above = suffix - local;  // digits of higher lanes
-    uint32_t digit = 0, above_digit = 0;
-    bool found = false;
-#pragma unroll
-    for (int j = 3; j >= 0; --j) {
-      if (above < need && above + c[j] >= need) {
-        digit = (uint32_t)(4 * lane + j);
-        above_digit = above;
-        found = true;
+      for (int e = 0; e < E; ++e)
+        if (valid[e] && (key[e] & mask) == prefix) {
+          const uint32_t rd = (uint32_t)(kBins - 1) - ((uint32_t)(key[e] >> shift) & dbits);
+          atomicAdd(&hist[rd + rd / kGroupBins], 1u);
+        }
+      __syncthreads();
+      {  // group totals: wave w sums groups 4 w .. 4 w + 3, two bins per lane
+        const int gq = 4 * wave + lane / 16, j0 = 2 * (lane % 16);
+        const uint32_t part = row_sum16(hist[gq * kGroupStride + j0] + hist[gq * kGroupStride + j0 + 1]);
+        if (lane % 16 == 0) grp[gq] = part;
       }
-      above += c[j];
+      __syncthreads();
+      const uint32_t gc = grp[lane];
+      const uint32_t gincl = wave_inclusive_scan(gc);
+      const int g = min((int)__builtin_ctzll(__ballot(gincl >= need)), kWave - 1);
+      const uint32_t gabove = (uint32_t)__builtin_amdgcn_readlane((int)(gincl - gc), g);
+      const uint32_t dc = lane < kGroupBins ? hist[g * kGroupStride + lane] : 0u;
+      const uint32_t dincl = wave_inclusive_scan(dc) + gabove;
+      const int j = min((int)__builtin_ctzll(__ballot(dincl >= need)), kGroupBins - 1);
+      const uint32_t cnt = (uint32_t)__builtin_amdgcn_readlane((int)dc, j);
+      const uint32_t above = (uint32_t)__builtin_amdgcn_readlane((int)dincl, j) - cnt;
+      const uint32_t digit = (uint32_t)(kBins - 1) - (uint32_t)(g * kGroupBins + j);
+      prefix |= (uint64_t)digit << shift;
+      mask |= (uint64_t)dbits << shift;
+      need -= above;
+      if (cnt == need || shift == 0) break;
     }
-    const int src = (int)__builtin_ctzll(__ballot(found));
-    prefix |= (uint32_t)__builtin_amdgcn_readlane((int)digit, src) << shift;
-    mask |= dmask << shift;
-    need -= (uint32_t)__builtin_amdgcn_readlane((int)above_digit, src);
   }
   // Stable compaction in position order.
-  uint32_t eq = 0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) eq += (valid[e] && key[e] == prefix) ? 1u : 0u;
-  uint32_t total;
-  uint32_t tie_rank = block_exclusive_scan(eq, s_wave, total);
-  uint32_t sel = 0;
   bool take[E];
+  uint64_t bal[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const bool tie = valid[e] && key[e] == prefix;
-    take[e] = valid[e] && (key[e] > prefix || (tie && tie_rank < need));
-    tie_rank += tie ? 1u : 0u;
-    sel += take[e] ? 1u : 0u;
+    take[e] = valid[e] && (key[e] & mask) >= prefix;
+    bal[e] = __ballot(take[e]);
   }
-  uint32_t rank = block_exclusive_scan(sel, s_wave, total);
+  uint32_t mine = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) mine = lane == e ? (uint32_t)__popcll(bal[e]) : mine;
+  if (lane < E) s_cnt[lane * kWaves + wave] = mine;
+  __syncthreads();
+  const uint32_t c = s_cnt[lane];
+  const uint32_t excl = wave_inclusive_scan(c) - c;
+  int64_t* orow = out + (int64_t)blockIdx.x * m;
 #pragma unroll
   for (int e = 0; e < E; ++e)
     if (take[e]) {
-      out[(int64_t)blockIdx.x * m + rank] = E * tid + e;
-      s_sel[rank] = (uint32_t)(E * tid + e);
-      ++rank;
+      const uint32_t r = (uint32_t)__builtin_amdgcn_readlane((int)excl, e * kWaves + wave) +
+                         __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
+      const int p = e * kThreads + tid;
+      orow[r] = p;
+      if (tables) {
+        s_beg[r] = beg[e];
+        s_len[r] = (uint32_t)(end[e] - beg[e]);
+      }
     }
-  (void)lane;
-  if (tab.d_info == nullptr) return;
-  // The rescoring pass's tables of this row (group), from the positions in
+  if (!tables) return;
+  // The rescoring pass's tables of this row (group), from the token ranges in
   // LDS: one thread per wave of the pass.
   __syncthreads();
-  for (int64_t w = tid; w < tab.waves; w += blockDim.x)
-    candidate_wave_tables([&](int64_t i) { return (int64_t)s_sel[i]; }, m, (int64_t)blockIdx.x, tab.d_offsets,
-                          tab.waves, w, tab.per_wave, tab.cap, tab.d_info, tab.d_tiles);
+  for (int64_t w = tid; w < tab.waves; w += kThreads)
+    candidate_wave_tables(
+        [&](int64_t i, int64_t& b, int64_t& e) {
+          b = s_beg[i];
+          e = b + s_len[i];
+        },
+        m, (int64_t)blockIdx.x, tab.waves, w, tab.per_wave, tab.cap, tab.d_info, tab.d_tiles);
 }
 
 }  // namespace

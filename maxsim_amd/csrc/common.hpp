@@ -141,6 +141,19 @@ __device__ __forceinline__ uint32_t quad_broadcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, I * 0x55, 0xF, 0xF, false);
 }
 
+// Wait states between a block of MFMAs and the first VALU reads of their
+// results.  After v_mfma_i32_16x16x64_i8 the compiler's hazard model spaces a
+// dependent VALU read 8 wait states behind the MFMA; on gfx950 reads at that
+// distance returned the accumulator's earlier contents now and then
+// (nondeterministic scores, depending on how the waves of a SIMD
+// interleave).  24 more are added here, the scheduler kept from moving work
+// across them.
+__device__ __forceinline__ void mfma_results_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Whole-wave reduction: DPP quad butterflies and row rotations by 4 and 8
 // reduce each row of 16 lanes, then the four row results are combined from
 // lanes 0, 16, 32 and 48.  The result is wave-uniform.

@@ -209,11 +209,16 @@ __global__ __launch_bounds__(256) void int8q_maxsim_kernel(Int8qArgs p) {
       }
       const int64_t rem = len - t0;  // valid rows in this tile (>= 1)
       const int row0 = 4 * g;
+      v4i accs[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        accs[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], (v4i){bias[j], bias[j], bias[j], bias[j]}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) accs[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], accs[j], 0, 0, 0);
+      mfma_results_fence();
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        v4i acc = {bias[j], bias[j], bias[j], bias[j]};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(lo, blo[j], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(hi, bhi[j], acc, 0, 0, 0);
+        const v4i acc = accs[j];
         float x0 = (float)acc[0], x1 = (float)acc[1], x2 = (float)acc[2], x3 = (float)acc[3];
         if (kTokenScale) {
           x0 = x0 * s0;

@@ -500,6 +500,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       epi_p = epi_q;
     };
     auto last = [&](const v4i (&acc_p)[NT]) {
+      mfma_results_fence();  // the last tile's MFMAs were issued just before
       epilogue(acc_p, epi_p);
       finish((int)(mhi_p >> 8));  // the last tile always ends a document
     };

@@ -178,6 +178,11 @@ struct ScoreArgs {
   float rmul;
   const int64_t* wave_info;    // [groups][num_waves][kScoreInfoWords]
   const uint64_t* tiles;
+  // Direct mode (wave_info / tiles unused): wave w of a group scores target w
+  // (w < direct_count), the document targets[w] whose tokens are
+  // [direct_offsets[doc], direct_offsets[doc + 1]).
+  const int64_t* direct_offsets;
+  int64_t direct_count;
   int64_t num_waves;           // per group, a multiple of 4
   int64_t info_grp_stride;     // int64 words between groups' wave tables (0 = shared)
   const int64_t* targets;      // document of each target, or nullptr (target = document)

@@ -22,8 +22,9 @@
 // pass (int8 MFMA 5 POPS vs 157 TFLOP/s fp32).  An int8 query uses one limb.
 //
 // Work split: a wave owns a range of targets (documents, or candidate
-// positions) and walks their 16-token tiles from a host-built table; a tile
-// is the MFMA A operand (16 tokens x 128 dims), the query rows of the pass
+// positions) and walks their 16-token tiles from a table (or, in direct
+// mode, one candidate per wave, the tiles of its document's token range); a
+// tile is the MFMA A operand (16 tokens x 128 dims), the query rows of the pass
 // are B operands held in registers.  Each lane keeps the reducer state of
 // its query column over its four token rows; at a target's last tile the
 // four lane groups are merged and the per-row pooled values are written to
@@ -188,7 +189,7 @@ __device__ __forceinline__ void unpack_a_int4_order(const TileCodes<kDocSign>& t
 // running maximum is kept on the int32 accumulators and converted once per
 // document.
 template <int DOC, bool RES, int L, int NT, int RED, bool INTMAX>
-__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
+__global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreArgs p) {
   static_assert(!INTMAX || (DOC == kDocSign && !RES && L == 1 && RED == kRedMax), "integer maximum form");
   __shared__ float s_pool[kWavesPerGroup][16 * NT];
   const int lane = lane_id();
@@ -196,12 +197,36 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
   const int g = lane >> 4, c = lane & 15;
   const int grp = (int)blockIdx.y / p.subs, sub = (int)blockIdx.y % p.subs;
   const int64_t gw = (int64_t)blockIdx.x * kWavesPerGroup + wave;
-  const auto info = as_constant(p.wave_info) + grp * p.info_grp_stride + gw * kScoreInfoWords;
-  const int64_t t0 = info[0];
-  const int ntiles = (int)info[2];
-  if (ntiles == 0) return;  // no barriers below: a wave may leave early
-  const auto tt = as_constant(p.tiles) + info[3];
   const auto targets = p.targets ? as_constant(p.targets) + grp * p.targets_grp_stride : nullptr;
+  // Table mode: the wave's first target, tile count and tiles from the
+  // tables.  Direct mode: target gw of the group, its tiles from the token
+  // range of its document.
+  const bool direct = p.direct_offsets != nullptr;
+  int64_t t0, ds = 0, de = 0;
+  int ntiles;
+  const __attribute__((address_space(4))) uint64_t* tt = nullptr;
+  if (direct) {
+    if (gw >= p.direct_count) return;  // no barriers below: a wave may leave early
+    t0 = gw;
+    const int64_t doc = targets[gw];
+    ds = as_constant(p.direct_offsets)[doc];
+    de = as_constant(p.direct_offsets)[doc + 1];
+    ntiles = ds == de ? 1 : (int)((de - ds + 15) / 16);
+  } else {
+    const auto info = as_constant(p.wave_info) + grp * p.info_grp_stride + gw * kScoreInfoWords;
+    t0 = info[0];
+    ntiles = (int)info[2];
+    if (ntiles == 0) return;
+    tt = as_constant(p.tiles) + info[3];
+  }
+  // Tile i of the wave (i >= ntiles: a padding entry at token 0).
+  auto entry = [&](int i) -> uint64_t {
+    if (i >= ntiles) return score_tile_entry(0, 1, false, false, 0);
+    if (!direct) return tt[i];
+    if (ds == de) return score_tile_entry(0, 1, true, true, 0);
+    const int64_t x = ds + 16 * (int64_t)i;
+    return score_tile_entry(x, min<int64_t>(16, de - x), x + 16 >= de, false, 0);
+  };
   const auto doc_scale = p.doc_scale ? as_constant(p.doc_scale) : nullptr;
   const int lr0 = sub * 16 * NT;                           // first local row of the pass
   const int64_t grow0 = (int64_t)grp * p.grp_rows + lr0;  // its global query row
@@ -250,24 +275,24 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
       t.a.w = *reinterpret_cast<const unsigned*>(p.codes + tok * 16 + 4 * g);
     if constexpr (RES) t.r.w = *reinterpret_cast<const v4u*>(p.rcodes + tok * 64 + 16 * g);
     if constexpr (!INTMAX) {
+      // Token rows 4g .. 4g + 3 in one load; rows past the tile read 0
+      // (buffer bounds at the tile's last row; they are masked below).
+      const uint32_t nbytes = (uint32_t)(rows1 + 1) * 4u;
+      const v4u sv = load_b128(make_rsrc(p.tscale + start, nbytes), 16 * g);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int64_t tr = start + min(4 * g + rr, rows1);
-        t.s[rr] = p.tscale[tr];
-        if constexpr (RES) t.sr[rr] = p.rtscale[tr];
+      for (int rr = 0; rr < 4; ++rr) t.s[rr] = __uint_as_float(sv[rr]);
+      if constexpr (RES) {
+        const v4u rv = load_b128(make_rsrc(p.rtscale + start, nbytes), 16 * g);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) t.sr[rr] = __uint_as_float(rv[rr]);
       }
     }
   };
 
-  Tile cur, nxt;
-  uint64_t e = tt[0];
-  load(e, cur);
   int len = 0;  // tokens of the current target seen so far (wave-uniform)
   float dscale = 1.0f;
   bool fresh = true;
-  for (int i = 0; i < ntiles; ++i) {
-    const uint64_t en = tt[i + 1];
-    load(en, nxt);
+  auto step = [&](const uint64_t e, const Tile& cur) __attribute__((always_inline)) {
     const int local = (int)(e >> kTileLocalShift);
     const bool last = ((e >> kTileLastShift) & 1) != 0;
     const int rows = ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
@@ -313,6 +338,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
         for (int l = 0; l < L; ++l)
           accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], accr[l][j], 0, 0, 0);
     }
+    mfma_results_fence();
 
     if constexpr (INTMAX) {
 #pragma unroll
@@ -423,8 +449,29 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs p) {
       len = 0;
     }
     fresh = last;
-    cur = nxt;
-    e = en;
+  };
+
+  // A ring of kAhead + 1 tiles: tile i is in slot i % (kAhead + 1), and the
+  // loads of tile i + kAhead are issued before tile i is computed.  Waves of
+  // the two-tile passes (candidate rescoring: few waves per SIMD, short
+  // documents) keep three tiles in flight; the larger passes one.
+  constexpr int kAhead = NT <= 2 ? 3 : 1;
+  Tile ring[kAhead + 1];
+  uint64_t ent[kAhead + 1];
+#pragma unroll
+  for (int u = 0; u < kAhead; ++u) {
+    ent[u] = entry(u);
+    load(ent[u], ring[u]);
+  }
+  for (int i0 = 0; i0 < ntiles; i0 += kAhead + 1) {
+#pragma unroll
+    for (int u = 0; u <= kAhead; ++u) {
+      if (i0 + u >= ntiles) break;
+      const int sl = (u + kAhead) % (kAhead + 1);
+      ent[sl] = entry(i0 + u + kAhead);
+      load(ent[sl], ring[sl]);
+      step(ent[u], ring[u]);
+    }
   }
 }
 

@@ -143,80 +143,120 @@ __global__ __launch_bounds__(THREADS) void topk_small_kernel(const float* __rest
 }
 
 // ------------------------------------------------------ threshold filter
-// k <= kSmallTopkMaxK and n <= kFilterThreads * kFilterEPT.  Element i of the
-// row goes to thread i % 1024 (coalesced loads).  In each wave, T_w = the
-// k-th largest of the 64 lanes' maximum keys: the wave holds at least k keys
-// >= T_w, so every key of the row's top k is >= T = max_w T_w.  At most k
-// lanes per wave have a maximum >= T (keys are unique), so at most
-// kFilterEPT * k keys per wave pass the filter; wave 0 selects the k best of
-// them in k rounds of a wave maximum.
-constexpr int kFilterThreads = 1024;
-constexpr int kFilterEPT = 4;
+// k <= kSmallTopkMaxK and n <= kFilterThreads * EPT: four waves, element i of
+// the row in thread i % 256 (coalesced loads; the id map, when given, loaded
+// beside the scores).  Keys are 64-bit, order-preserving score bits above
+// 2^32 - 1 - position, so every key is distinct and a larger key is a higher
+// score or, on a tie, a lower position.  In each wave, T_w = the k-th largest
+// of the 64 lanes' maximum keys (a radix selection by ballot counts, no
+// shuffles): k lanes of the wave hold a key >= T_w, so every key of the row's
+// top k is >= T = max_w T_w.  At most k lanes per wave have a maximum >= T,
+// so at most 4 * k * EPT keys pass the filter; they go to a list in LDS
+// (one atomic per wave for its range, ballot offsets inside it) with their
+// float bits and ids, and each one's rank is counted against the list.
+// kCap is a multiple of eight.  The key of rank r < k is written to slot r.
+constexpr int kFilterThreads = 256;
 constexpr int kFilterWaves = kFilterThreads / kWave;
-constexpr int kFilterCap = kFilterWaves * kFilterEPT * kSmallTopkMaxK;
 
+// The k-th largest of the wave's nonzero keys (wave-uniform), 0 when fewer
+// than k lanes hold one.  The low 32 bits of every nonzero key are >= 2^32 -
+// 4096 (positions below 4096), so those 20 bits of the result need no step.
+__device__ __forceinline__ uint64_t wave_kth_largest_key(uint64_t x, int k) {
+  if (__popcll(__ballot(x != 0)) < k) return 0;
+  uint64_t t = 0;
+#pragma unroll
+  for (int bit = 63; bit >= 32; --bit) {
+    const uint64_t c = t | (1ull << bit);
+    t = __popcll(__ballot(x >= c)) >= k ? c : t;
+  }
+  t |= 0xFFFFF000ull;
+#pragma unroll
+  for (int bit = 11; bit >= 0; --bit) {
+    const uint64_t c = t | (1ull << bit);
+    t = __popcll(__ballot(x >= c)) >= k ? c : t;
+  }
+  return t;
+}
+
+template <int EPT>
 __global__ __launch_bounds__(kFilterThreads) void topk_filter_kernel(const float* __restrict__ scores, int64_t n,
                                                                      int64_t row_stride, int32_t k,
                                                                      const int64_t* __restrict__ id_map,
                                                                      float* __restrict__ out_scores,
                                                                      int64_t* __restrict__ out_ids) {
-  __shared__ uint64_t s_cand[kFilterCap];
+  constexpr int kCap = kFilterWaves * kSmallTopkMaxK * EPT;
+  static_assert(kCap % 8 == 0, "rank steps of eight keys");
+  __shared__ uint64_t s_key[kCap];
+  __shared__ int64_t s_id[kCap];
+  __shared__ uint32_t s_raw[kCap];
   __shared__ uint64_t s_thr[kFilterWaves];
-  __shared__ uint64_t s_best[kSmallTopkMaxK];
   __shared__ uint32_t s_count;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int64_t b = blockIdx.x;
-  const float* row = scores + b * row_stride;
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(row, (uint32_t)(n * 4));
-  float v[kFilterEPT];
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(scores + b * row_stride, (uint32_t)(n * 4));
+  const __amdgpu_buffer_rsrc_t rid = make_rsrc(id_map ? id_map + b * n : nullptr, id_map ? (uint32_t)(n * 8) : 0u);
+  uint32_t v[EPT];
+  int64_t id[EPT];
 #pragma unroll
-  for (int e = 0; e < kFilterEPT; ++e) v[e] = __uint_as_float(load_b32(rsrc, (e * kFilterThreads + tid) * 4));
+  for (int e = 0; e < EPT; ++e) v[e] = load_b32(rsrc, (e * kFilterThreads + tid) * 4);
+  if (id_map) {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) id[e] = (int64_t)load_b64(rid, (e * kFilterThreads + tid) * 8);
+  }
   if (tid == 0) s_count = 0;
-  uint64_t key[kFilterEPT], lmax = 0;
+  for (int i = tid; i < kCap; i += kFilterThreads) s_key[i] = 0u;
+  uint64_t key[EPT], lmax = 0;
 #pragma unroll
-  for (int e = 0; e < kFilterEPT; ++e) {
+  for (int e = 0; e < EPT; ++e) {
     const int i = e * kFilterThreads + tid;
-    key[e] = i < n ? ((uint64_t)score_key(v[e]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0u;
+    key[e] = i < n ? ((uint64_t)score_key(__uint_as_float(v[e])) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0u;
     lmax = key[e] > lmax ? key[e] : lmax;
   }
-  // T_w: k rounds of the wave maximum over the lanes' maxima.
-  uint64_t m = lmax, kth = 0;
-  for (int r = 0; r < k; ++r) {
-    kth = wave_max_u64(m);
-    if (m == kth) m = 0;
-  }
-  if (lane == 0) s_thr[wave] = kth;
+  const uint64_t tw = wave_kth_largest_key(lmax, k);
+  if (lane == 0) s_thr[wave] = tw;
   __syncthreads();
   uint64_t t = 0;
 #pragma unroll
   for (int w = 0; w < kFilterWaves; ++w) t = s_thr[w] > t ? s_thr[w] : t;
+  uint64_t mask[EPT];
+  uint32_t cnt = 0;
 #pragma unroll
-  for (int e = 0; e < kFilterEPT; ++e) {
-    if (key[e] != 0 && key[e] >= t) s_cand[atomicAdd(&s_count, 1u)] = key[e];
+  for (int e = 0; e < EPT; ++e) {
+    mask[e] = __ballot(key[e] != 0 && key[e] >= t);
+    cnt += (uint32_t)__popcll(mask[e]);
   }
-  __syncthreads();
-  if (wave == 0) {
-    const int c = (int)s_count;
-    for (int r = 0; r < k; ++r) {
-      uint64_t best = 0;
-      int slot = -1;
-      for (int j = lane; j < c; j += kWave) {
-        const uint64_t x = s_cand[j];
-        if (x > best) {
-          best = x;
-          slot = j;
-        }
-      }
-      const uint64_t top = wave_max_u64(best);
-      if (slot >= 0 && best == top) s_cand[slot] = 0;  // the one lane holding it drops it
-      if (lane == 0) s_best[r] = top;
+  uint32_t base = 0;
+  if (lane == 0 && cnt != 0) base = atomicAdd(&s_count, cnt);
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if ((mask[e] >> lane) & 1ull) {
+      const uint32_t at =
+          base + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask[e], 0u));
+      s_key[at] = key[e];
+      s_raw[at] = v[e];
+      if (id_map) s_id[at] = id[e];
     }
+    base += (uint32_t)__popcll(mask[e]);
   }
   __syncthreads();
-  if (tid < k) {
-    const int64_t pos = (int64_t)(0xFFFFFFFFu - (uint32_t)s_best[tid]);
-    out_scores[b * k + tid] = row[pos];
-    out_ids[b * k + tid] = id_map ? id_map[b * n + pos] : pos;
+  // Ranks, counted against the whole list (broadcast LDS reads, eight keys
+  // per step; the zeroed tail pads the list to a multiple of eight).
+  const int c = (int)s_count, c8 = (c + 7) & ~7;
+  for (int i = tid; i < c; i += kFilterThreads) {
+    const uint64_t x = s_key[i];
+    int r = 0;
+    for (int j = 0; j < c8; j += 8) {
+      uint64_t y[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) y[u] = s_key[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) r += y[u] > x ? 1 : 0;
+    }
+    if (r < k) {
+      out_scores[b * k + r] = __uint_as_float(s_raw[i]);
+      out_ids[b * k + r] = id_map ? s_id[i] : (int64_t)(0xFFFFFFFFu - (uint32_t)x);
+    }
   }
 }
 
@@ -225,9 +265,20 @@ hipError_t launch_topk(const float* d_scores, int64_t batch, int64_t n, int64_t 
                        int64_t* d_out_ids, hipStream_t stream) {
   if (batch == 0 || k == 0) return hipSuccess;
   if (k > kTopkMaxK || k > n) return hipErrorInvalidValue;
-  if (k <= kSmallTopkMaxK && n <= kFilterThreads * kFilterEPT) {
-    topk_filter_kernel<<<dim3((unsigned)batch), dim3(kFilterThreads), 0, stream>>>(
-        d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);
+  if (k <= kSmallTopkMaxK && n <= kFilterThreads * 16) {
+    const dim3 grid((unsigned)batch), block(kFilterThreads);
+    if (n <= kFilterThreads * 2)
+      topk_filter_kernel<2><<<grid, block, 0, stream>>>(d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores,
+                                                        d_out_ids);
+    else if (n <= kFilterThreads * 4)
+      topk_filter_kernel<4><<<grid, block, 0, stream>>>(d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores,
+                                                        d_out_ids);
+    else if (n <= kFilterThreads * 8)
+      topk_filter_kernel<8><<<grid, block, 0, stream>>>(d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores,
+                                                        d_out_ids);
+    else
+      topk_filter_kernel<16><<<grid, block, 0, stream>>>(d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores,
+                                                         d_out_ids);
   } else if (k <= kSmallTopkMaxK && n <= 1024 * kSmallEPT) {
     topk_small_kernel<1024><<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(
         d_scores, n, row_stride, (int32_t)k, d_id_map, d_out_scores, d_out_ids);

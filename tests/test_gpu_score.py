@@ -369,3 +369,33 @@ def test_maxsim_cuda_free_functions_match_reference_lut(gpu, oracle):
     _close(batch, np.stack([oracle.binary_lut_maxsim(qb, codes, offsets, 128) for qb in query]))
     np.testing.assert_array_equal(batch, h.maxsim_batch(query))
     np.testing.assert_array_equal(_maxsim_hip.maxsim_cuda(query[1], codes, offsets, 128), batch[1])
+
+
+@pytest.mark.parametrize("reducer", ["maxsim", "topk2", "topk4", "smoothsim"])
+def test_scores_repeat_and_agree_across_row_splits(gpu, reducer):
+    """The same documents scored for four batch rows at once (passes of 64 or
+    128 query rows) and for one row at a time (passes of 32 rows) run
+    different kernel instantiations over identical per-row arithmetic, so the
+    scores must agree bit for bit, and repeating a call must reproduce them.
+    Multi-tile documents (up to 150 tokens) exercise the tile look-ahead; a
+    read of an MFMA accumulator before its result lands shows up here as
+    small, run-to-run varying differences."""
+    from maxsim_amd import synthetic
+    from maxsim_amd.binres import binres_score, binres_to_device, pack_binary_residual
+    from maxsim_amd.cascade import pack_residual_int4, residual_int4_to_device, residual_score
+
+    c = synthetic.make_corpus(300, 1, 150, seed=77)
+    query = synthetic.make_queries(c, 4)
+    p = residual_int4_to_device(pack_residual_int4(c.embeddings, c.offsets))
+    full = residual_score(query, p, reducer=reducer, temperature=0.7)
+    for _ in range(3):
+        np.testing.assert_array_equal(residual_score(query, p, reducer=reducer, temperature=0.7), full)
+        rows = np.stack([residual_score(query[r:r + 1], p, reducer=reducer, temperature=0.7)[0] for r in range(4)])
+        np.testing.assert_array_equal(rows, full)
+    if reducer == "maxsim":
+        b = binres_to_device(pack_binary_residual(c.embeddings, c.offsets))
+        for fused in (False, True):
+            ref = binres_score(query, b, fused=fused)
+            for _ in range(3):
+                rows = np.stack([binres_score(query[r:r + 1], b, fused=fused)[0] for r in range(4)])
+                np.testing.assert_array_equal(rows, ref)
