@@ -292,10 +292,56 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   int len = 0;  // tokens of the current target seen so far (wave-uniform)
   float dscale = 1.0f;
   bool fresh = true;
-  auto step = [&](const uint64_t e, const Tile& cur) __attribute__((always_inline)) {
+
+  // Accumulators of one tile, and what its epilogue needs once its ring slot
+  // is reused.
+  struct Acc {
+    v4i s[L][NT];
+    v4i r[RES ? L : 1][RES ? NT : 1];
+  };
+  struct Pend {
+    uint64_t e;
+    float s[4], sr[4];
+  };
+  auto pend_of = [&](uint64_t e, const Tile& t) {
+    Pend q;
+    q.e = e;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      q.s[rr] = t.s[rr];
+      q.sr[rr] = RES ? t.sr[rr] : 0.0f;
+    }
+    return q;
+  };
+  struct Ops {
+    v4i a0, a1, r0, r1;
+  };
+  auto unpack = [&](const Tile& t) {
+    Ops o;
+    if constexpr (DOC == kDocSign && RES)
+      unpack_a_int4_order(t.a, o.a0, o.a1);
+    else
+      unpack_a(t.a, o.a0, o.a1);
+    if constexpr (RES) unpack_a(t.r, o.r0, o.r1);
+    return o;
+  };
+  // MFMAs of K half h of row block j (h = 0 starts from zero).
+  auto mfma_half = [&](Acc& A, const Ops& o, int h, int j) __attribute__((always_inline)) {
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+      A.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][j][h], h ? A.s[l][j] : zero, 0, 0, 0);
+    if constexpr (RES) {
+#pragma unroll
+      for (int l = 0; l < L; ++l)
+        A.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.r1 : o.r0, bq[l][j][h], h ? A.r[l][j] : zero, 0, 0, 0);
+    }
+  };
+  // Start of a tile's epilogue: its row count, and the document constants
+  // when it is its target's first tile.
+  auto begin_tile = [&](const Pend& P) __attribute__((always_inline)) {
+    const uint64_t e = P.e;
     const int local = (int)(e >> kTileLocalShift);
-    const bool last = ((e >> kTileLastShift) & 1) != 0;
-    const int rows = ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
     if (fresh) {
       const int64_t tg = t0 + local;
       const int64_t doc = targets ? targets[tg] : tg;
@@ -305,61 +351,19 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
         for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale;
       }
     }
-
-    v4i a0, a1;
-    if constexpr (DOC == kDocSign && RES)
-      unpack_a_int4_order(cur.a, a0, a1);
-    else
-      unpack_a(cur.a, a0, a1);
-    // All first halves, then all second halves: consecutive MFMAs are
-    // independent, so the matrix pipe never waits on its own result.
-    v4i acc[L][NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int l = 0; l < L; ++l)
-        acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int l = 0; l < L; ++l) acc[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], acc[l][j], 0, 0, 0);
-    v4i accr[RES ? L : 1][RES ? NT : 1];
-    if constexpr (RES) {
-      v4i r0, r1;
-      unpack_a(cur.r, r0, r1);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int l = 0; l < L; ++l)
-          accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][0], (v4i){0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int l = 0; l < L; ++l)
-          accr[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], accr[l][j], 0, 0, 0);
-    }
-    mfma_results_fence();
-
+    return ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
+  };
+  // Epilogue of row block j of a tile.
+  auto epi_j = [&](const Acc& A, const Pend& P, int rows, int j) __attribute__((always_inline)) {
     if constexpr (INTMAX) {
+      v4i a = A.s[0][j];
+      if (rows < 16) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        v4i a = acc[0][j];
-        if (rows < 16) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            if (4 * g + rr >= rows) a[rr] = INT32_MIN;
-        }
-        imax[j] = max(max(imax[j], max(a[0], a[1])), max(a[2], a[3]));
+        for (int rr = 0; rr < 4; ++rr)
+          if (4 * g + rr >= rows) a[rr] = INT32_MIN;
       }
+      imax[j] = max(max(imax[j], max(a[0], a[1])), max(a[2], a[3]));
     } else {
-    float srow[4], srrow[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      srow[rr] = cur.s[rr] * p.tmul;
-      srrow[rr] = RES ? cur.sr[rr] * p.rmul : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
       float z[4];
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -374,24 +378,24 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
         };
         float Y;
         if constexpr (L == 3 && DOC == kDocInt4) {
-          Y = limbs3(acc);
+          Y = limbs3(A.s);
         } else {
           float y[L];
 #pragma unroll
           for (int l = 0; l < L; ++l)
-            y[l] = DOC == kDocSign ? (float)(2 * acc[l][j][rr] - qsum[l][j]) : (float)acc[l][j][rr];
+            y[l] = DOC == kDocSign ? (float)(2 * A.s[l][j][rr] - qsum[l][j]) : (float)A.s[l][j][rr];
           Y = y[0];
           if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
         }
-        z[rr] = Y * srow[rr];
+        z[rr] = Y * (P.s[rr] * p.tmul);
         if constexpr (RES) {
           float YR;
           if constexpr (L == 3) {
-            YR = limbs3(accr);
+            YR = limbs3(A.r);
           } else {
-            YR = (float)accr[0][j][rr];
+            YR = (float)A.r[0][j][rr];
           }
-          z[rr] = z[rr] + YR * srrow[rr];
+          z[rr] = z[rr] + YR * (P.sr[rr] * p.rmul);
         }
       }
       if (rows < 16) {
@@ -401,9 +405,13 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
       }
       st[j].add4(z, k2);
     }
-    }
+  };
+  // End of a tile's epilogue: at its target's last tile, the target's score.
+  auto end_tile = [&](const Pend& P, int rows) __attribute__((always_inline)) {
+    const uint64_t e = P.e;
+    const int local = (int)(e >> kTileLocalShift);
+    const bool last = ((e >> kTileLastShift) & 1) != 0;
     len += rows;
-
     if (last) {
       const int64_t tg = t0 + local;
       float v[NT];
@@ -450,27 +458,140 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     }
     fresh = last;
   };
+  // The whole epilogue of a tile whose MFMAs were issued just before.
+  auto consume_now = [&](const Acc& A, const Pend& P) __attribute__((always_inline)) {
+    mfma_results_fence();
+    const int rows = begin_tile(P);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) epi_j(A, P, rows, j);
+    end_tile(P, rows);
+  };
+  // Pipelined form: the MFMAs of tile q, the epilogue of the previous tile p
+  // (its accumulators a whole tile old) interleaved with q's second halves.
+  auto issue_consume = [&](Acc& Q, const Tile& tq, const Acc& A, const Pend& P) __attribute__((always_inline)) {
+    const Ops o = unpack(tq);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) mfma_half(Q, o, 0, j);
+    const int rows = begin_tile(P);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      mfma_half(Q, o, 1, j);
+      epi_j(A, P, rows, j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    end_tile(P, rows);
+  };
+  // All MFMAs of a tile: the first stream's halves, then the residual's
+  // (its operands unpacked only then, so fewer registers are live).
+  auto issue = [&](Acc& Q, const Tile& tq) __attribute__((always_inline)) {
+    const v4i zero = {0, 0, 0, 0};
+    v4i a0, a1;
+    if constexpr (DOC == kDocSign && RES)
+      unpack_a_int4_order(tq.a, a0, a1);
+    else
+      unpack_a(tq.a, a0, a1);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int l = 0; l < L; ++l) Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][0], zero, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int l = 0; l < L; ++l) Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], Q.s[l][j], 0, 0, 0);
+    if constexpr (RES) {
+      v4i r0, r1;
+      unpack_a(tq.r, r0, r1);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int l = 0; l < L; ++l) Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][0], zero, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int l = 0; l < L; ++l) Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], Q.r[l][j], 0, 0, 0);
+    }
+  };
 
-  // A ring of kAhead + 1 tiles: tile i is in slot i % (kAhead + 1), and the
-  // loads of tile i + kAhead are issued before tile i is computed.  Waves of
-  // the two-tile passes (candidate rescoring: few waves per SIMD, short
-  // documents) keep three tiles in flight; the larger passes one.
-  constexpr int kAhead = NT <= 2 ? 3 : 1;
-  Tile ring[kAhead + 1];
-  uint64_t ent[kAhead + 1];
+  // Passes of eight row blocks keep one tile in flight (registers); the
+  // loop is kept simple (a tight loop over a document's tiles), and each tile
+  // fences its MFMAs.
+  if constexpr (NT > 2) {
+    Tile cur, nxt;
+    auto run = [&](auto next) __attribute__((always_inline)) {
+      uint64_t e = next(0);
+      load(e, cur);
+      for (int i = 0; i < ntiles; ++i) {
+        const uint64_t en = next(i + 1);
+        load(en, nxt);
+        Acc a;
+        issue(a, cur);
+        consume_now(a, pend_of(e, cur));
+        cur = nxt;
+        e = en;
+      }
+    };
+    if (direct)
+      run(entry);
+    else
+      run([&](int i) -> uint64_t { return tt[i]; });  // i <= ntiles: the table's padding entry last
+  } else {
+    // Two-tile passes (candidate rescoring: few waves per SIMD, short
+    // documents): a ring of kAhead + 1 tiles, tile i in slot i % (kAhead + 1),
+    // the loads of tile i + kAhead issued before tile i is computed.
+    constexpr int kAhead = 3;
+    static_assert((kAhead + 1) % 2 == 0, "tiles alternate between two accumulator sets");
+    // One-limb passes interleave each tile's epilogue with the next tile's
+    // MFMAs (two accumulator sets); three-limb passes would lose occupancy
+    // to the second set and fence each tile instead.
+    constexpr bool kPipe = L == 1;
+    Tile ring[kAhead + 1];
+    uint64_t ent[kAhead + 1];
 #pragma unroll
-  for (int u = 0; u < kAhead; ++u) {
-    ent[u] = entry(u);
-    load(ent[u], ring[u]);
-  }
-  for (int i0 = 0; i0 < ntiles; i0 += kAhead + 1) {
+    for (int u = 0; u < kAhead; ++u) {
+      ent[u] = entry(u);
+      load(ent[u], ring[u]);
+    }
+    if constexpr (kPipe) {
+      Acc acc[2];
+      Pend pend[2];
+      // Tile 0.
+      ent[kAhead] = entry(kAhead);
+      load(ent[kAhead], ring[kAhead]);
+      pend[0] = pend_of(ent[0], ring[0]);
+      issue(acc[0], ring[0]);
+      // Tile i (i >= 1) is in slot (u + 1) % (kAhead + 1) and set (u + 1) % 2;
+      // its loads reuse the slot of tile i - 1, whose epilogue data is in pend.
+      for (int i0 = 1; i0 < ntiles; i0 += kAhead + 1) {
 #pragma unroll
-    for (int u = 0; u <= kAhead; ++u) {
-      if (i0 + u >= ntiles) break;
-      const int sl = (u + kAhead) % (kAhead + 1);
-      ent[sl] = entry(i0 + u + kAhead);
-      load(ent[sl], ring[sl]);
-      step(ent[u], ring[u]);
+        for (int u = 0; u <= kAhead; ++u) {
+          if (i0 + u >= ntiles) break;
+          const int sl = (u + 1) % (kAhead + 1), so = u % (kAhead + 1);
+          const int sq = (u + 1) % 2, sp = u % 2;
+          ent[so] = entry(i0 + u + kAhead);
+          load(ent[so], ring[so]);
+          pend[sq] = pend_of(ent[sl], ring[sl]);
+          issue_consume(acc[sq], ring[sl], acc[sp], pend[sp]);
+        }
+      }
+      if ((ntiles - 1) % 2 == 0)
+        consume_now(acc[0], pend[0]);
+      else
+        consume_now(acc[1], pend[1]);
+    } else {
+      for (int i0 = 0; i0 < ntiles; i0 += kAhead + 1) {
+#pragma unroll
+        for (int u = 0; u <= kAhead; ++u) {
+          if (i0 + u >= ntiles) break;
+          const int sl = (u + kAhead) % (kAhead + 1);
+          ent[sl] = entry(i0 + u + kAhead);
+          load(ent[sl], ring[sl]);
+          Acc a;
+          issue(a, ring[u]);
+          consume_now(a, pend_of(ent[u], ring[u]));
+        }
+      }
     }
   }
 }
