@@ -259,6 +259,7 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   }
 
   struct Tile {
+    uint64_t e;  // its table entry (table mode)
     TileCodes<DOC> a;
     TileCodes<kDocInt4> r;
     float s[4], sr[4];
@@ -266,6 +267,7 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   // Every load is unconditional: rows past a short document read its last
   // token again (masked below); table padding entries point at token 0.
   auto load = [&](uint64_t e, Tile& t) {
+    t.e = e;
     const int64_t start = (int64_t)(e & kTileStartMask);
     const int rows1 = (int)((e >> kTileRowsShift) & 15);
     const int64_t tok = start + min(c, rows1);
@@ -303,9 +305,9 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     uint64_t e;
     float s[4], sr[4];
   };
-  auto pend_of = [&](uint64_t e, const Tile& t) {
+  auto pend_of = [&](const Tile& t) {
     Pend q;
-    q.e = e;
+    q.e = t.e;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       q.s[rr] = t.s[rr];
@@ -406,74 +408,72 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
       st[j].add4(z, k2);
     }
   };
+  // Score of target tg from the reducer state over its `len` tokens.
+  auto finish_target = [&](int64_t tg) __attribute__((always_inline)) {
+    float v[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      if constexpr (INTMAX) {
+        int m = max(imax[j], __shfl_xor(imax[j], 16));
+        m = max(m, __shfl_xor(m, 32));
+        v[j] = len == 0 ? 0.0f : (float)(2 * m - qsum[0][j]) * colmul[j] * weight[j] * dscale;
+        imax[j] = INT32_MIN;
+      } else {
+        st[j].merge_xor(16, k2);
+        st[j].merge_xor(32, k2);
+        v[j] = st[j].finish(len, colmul[j], p.temperature, weight[j], dscale);
+        st[j].init();
+      }
+    }
+    if (p.out || p.iout) {
+      // Whole batch rows in this pass: sum each row's query tokens here
+      // (sequentially from its first token) and write the score.
+      if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) s_pool[wave][16 * j + c] = v[j];
+      }
+      wave_sync_lds();
+      const int nb = min(16 * NT, p.grp_rows - lr0) / p.query_tokens;
+      if (lane < nb) {
+        float sum = 0.0f;
+        for (int q = 0; q < p.query_tokens; ++q) sum += s_pool[wave][lane * p.query_tokens + q];
+        const int64_t b = (grow0 / p.query_tokens) + lane;
+        if (p.out) p.out[b * p.out_stride + tg] = sum;
+        if (p.iout) p.iout[b * p.iout_stride + tg] = (int32_t)sum;
+      }
+      wave_sync_lds();
+    } else {
+      float* out = p.pooled + grp * p.pooled_grp_stride + tg * p.grp_rows;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int lr = lr0 + 16 * j + c;
+        if (g == 0 && lr < p.grp_rows) out[lr] = v[j];
+      }
+    }
+    len = 0;
+  };
   // End of a tile's epilogue: at its target's last tile, the target's score.
   auto end_tile = [&](const Pend& P, int rows) __attribute__((always_inline)) {
     const uint64_t e = P.e;
-    const int local = (int)(e >> kTileLocalShift);
     const bool last = ((e >> kTileLastShift) & 1) != 0;
     len += rows;
-    if (last) {
-      const int64_t tg = t0 + local;
-      float v[NT];
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        if constexpr (INTMAX) {
-          int m = max(imax[j], __shfl_xor(imax[j], 16));
-          m = max(m, __shfl_xor(m, 32));
-          v[j] = len == 0 ? 0.0f : (float)(2 * m - qsum[0][j]) * colmul[j] * weight[j] * dscale;
-          imax[j] = INT32_MIN;
-        } else {
-          st[j].merge_xor(16, k2);
-          st[j].merge_xor(32, k2);
-          v[j] = st[j].finish(len, colmul[j], p.temperature, weight[j], dscale);
-          st[j].init();
-        }
-      }
-      if (p.out || p.iout) {
-        // Whole batch rows in this pass: sum each row's query tokens here
-        // (sequentially from its first token) and write the score.
-        if (g == 0) {
-#pragma unroll
-          for (int j = 0; j < NT; ++j) s_pool[wave][16 * j + c] = v[j];
-        }
-        wave_sync_lds();
-        const int nb = min(16 * NT, p.grp_rows - lr0) / p.query_tokens;
-        if (lane < nb) {
-          float sum = 0.0f;
-          for (int q = 0; q < p.query_tokens; ++q) sum += s_pool[wave][lane * p.query_tokens + q];
-          const int64_t b = (grow0 / p.query_tokens) + lane;
-          if (p.out) p.out[b * p.out_stride + tg] = sum;
-          if (p.iout) p.iout[b * p.iout_stride + tg] = (int32_t)sum;
-        }
-        wave_sync_lds();
-      } else {
-        float* out = p.pooled + grp * p.pooled_grp_stride + tg * p.grp_rows;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int lr = lr0 + 16 * j + c;
-          if (g == 0 && lr < p.grp_rows) out[lr] = v[j];
-        }
-      }
-      len = 0;
-    }
+    if (last) finish_target(t0 + (int)(e >> kTileLocalShift));
     fresh = last;
   };
-  // The whole epilogue of a tile whose MFMAs were issued just before.
-  auto consume_now = [&](const Acc& A, const Pend& P) __attribute__((always_inline)) {
+  // The epilogue of a tile whose MFMAs were issued just before.
+  auto consume_now = [&](const Acc& A, const Pend& P, int rows) __attribute__((always_inline)) {
     mfma_results_fence();
-    const int rows = begin_tile(P);
 #pragma unroll
     for (int j = 0; j < NT; ++j) epi_j(A, P, rows, j);
-    end_tile(P, rows);
   };
   // Pipelined form: the MFMAs of tile q, the epilogue of the previous tile p
   // (its accumulators a whole tile old) interleaved with q's second halves.
-  auto issue_consume = [&](Acc& Q, const Tile& tq, const Acc& A, const Pend& P) __attribute__((always_inline)) {
+  auto issue_consume = [&](Acc& Q, const Tile& tq, const Acc& A, const Pend& P, int rows)
+                           __attribute__((always_inline)) {
     const Ops o = unpack(tq);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NT; ++j) mfma_half(Q, o, 0, j);
-    const int rows = begin_tile(P);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -481,7 +481,6 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
       epi_j(A, P, rows, j);
       __builtin_amdgcn_sched_barrier(0);
     }
-    end_tile(P, rows);
   };
   // All MFMAs of a tile: the first stream's halves, then the residual's
   // (its operands unpacked only then, so fewer registers are live).
@@ -514,85 +513,133 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     }
   };
 
-  // Passes of eight row blocks keep one tile in flight (registers); the
-  // loop is kept simple (a tight loop over a document's tiles), and each tile
-  // fences its MFMAs.
-  if constexpr (NT > 2) {
-    Tile cur, nxt;
-    auto run = [&](auto next) __attribute__((always_inline)) {
-      uint64_t e = next(0);
-      load(e, cur);
-      for (int i = 0; i < ntiles; ++i) {
-        const uint64_t en = next(i + 1);
-        load(en, nxt);
-        Acc a;
-        issue(a, cur);
-        consume_now(a, pend_of(e, cur));
-        cur = nxt;
-        e = en;
-      }
-    };
-    if (direct)
-      run(entry);
-    else
-      run([&](int i) -> uint64_t { return tt[i]; });  // i <= ntiles: the table's padding entry last
-  } else {
-    // Two-tile passes (candidate rescoring: few waves per SIMD, short
-    // documents): a ring of kAhead + 1 tiles, tile i in slot i % (kAhead + 1),
-    // the loads of tile i + kAhead issued before tile i is computed.
-    constexpr int kAhead = 3;
-    static_assert((kAhead + 1) % 2 == 0, "tiles alternate between two accumulator sets");
-    // One-limb passes interleave each tile's epilogue with the next tile's
-    // MFMAs (two accumulator sets); three-limb passes would lose occupancy
-    // to the second set and fence each tile instead.
-    constexpr bool kPipe = L == 1;
+  // Tiles in flight (a ring of kAhead + 1, tile i in slot i % (kAhead + 1),
+  // the loads of tile i + kAhead issued before tile i is computed): three for
+  // the two-tile passes (candidate rescoring: few waves per SIMD, short
+  // documents), one for eight row blocks (registers).  One-limb two-tile
+  // passes interleave each tile's epilogue with the next tile's MFMAs (two
+  // accumulator sets); the others fence each tile.
+  constexpr int kAhead = NT <= 2 ? 3 : 1;
+  constexpr bool kPipe = NT <= 2 && L == 1;
+  static_assert(!kPipe || (kAhead + 1) % 2 == 0, "tiles alternate between two accumulator sets");
+
+  // The ring loop over tiles 0 .. n - 1: fetch(i, Tile&) issues tile i's
+  // loads (i >= n allowed), meta(i, Pend&) returns its row count after
+  // starting its epilogue, done(Pend&, rows) ends it.
+  auto run_ring = [&](int n, auto fetch, auto meta, auto done) __attribute__((always_inline)) {
     Tile ring[kAhead + 1];
-    uint64_t ent[kAhead + 1];
 #pragma unroll
-    for (int u = 0; u < kAhead; ++u) {
-      ent[u] = entry(u);
-      load(ent[u], ring[u]);
-    }
+    for (int u = 0; u < kAhead; ++u) fetch(u, ring[u]);
     if constexpr (kPipe) {
       Acc acc[2];
       Pend pend[2];
-      // Tile 0.
-      ent[kAhead] = entry(kAhead);
-      load(ent[kAhead], ring[kAhead]);
-      pend[0] = pend_of(ent[0], ring[0]);
+      fetch(kAhead, ring[kAhead]);
       issue(acc[0], ring[0]);
+      pend[0] = pend_of(ring[0]);
+      int rows_p = meta(0, pend[0]);
       // Tile i (i >= 1) is in slot (u + 1) % (kAhead + 1) and set (u + 1) % 2;
       // its loads reuse the slot of tile i - 1, whose epilogue data is in pend.
-      for (int i0 = 1; i0 < ntiles; i0 += kAhead + 1) {
+      for (int i0 = 1; i0 < n; i0 += kAhead + 1) {
 #pragma unroll
         for (int u = 0; u <= kAhead; ++u) {
-          if (i0 + u >= ntiles) break;
+          if (i0 + u >= n) break;
           const int sl = (u + 1) % (kAhead + 1), so = u % (kAhead + 1);
           const int sq = (u + 1) % 2, sp = u % 2;
-          ent[so] = entry(i0 + u + kAhead);
-          load(ent[so], ring[so]);
-          pend[sq] = pend_of(ent[sl], ring[sl]);
-          issue_consume(acc[sq], ring[sl], acc[sp], pend[sp]);
+          fetch(i0 + u + kAhead, ring[so]);
+          pend[sq] = pend_of(ring[sl]);
+          issue_consume(acc[sq], ring[sl], acc[sp], pend[sp], rows_p);
+          done(pend[sp], rows_p);
+          rows_p = meta(i0 + u, pend[sq]);
         }
       }
-      if ((ntiles - 1) % 2 == 0)
-        consume_now(acc[0], pend[0]);
-      else
-        consume_now(acc[1], pend[1]);
+      if ((n - 1) % 2 == 0) {
+        consume_now(acc[0], pend[0], rows_p);
+        done(pend[0], rows_p);
+      } else {
+        consume_now(acc[1], pend[1], rows_p);
+        done(pend[1], rows_p);
+      }
     } else {
-      for (int i0 = 0; i0 < ntiles; i0 += kAhead + 1) {
+      for (int i0 = 0; i0 < n; i0 += kAhead + 1) {
 #pragma unroll
         for (int u = 0; u <= kAhead; ++u) {
-          if (i0 + u >= ntiles) break;
-          const int sl = (u + kAhead) % (kAhead + 1);
-          ent[sl] = entry(i0 + u + kAhead);
-          load(ent[sl], ring[sl]);
+          if (i0 + u >= n) break;
+          fetch(i0 + u + kAhead, ring[(u + kAhead) % (kAhead + 1)]);
           Acc a;
           issue(a, ring[u]);
-          consume_now(a, pend_of(ent[u], ring[u]));
+          Pend P = pend_of(ring[u]);
+          const int rows = meta(i0 + u, P);
+          consume_now(a, P, rows);
+          done(P, rows);
         }
       }
     }
+  };
+
+  if (direct) {
+    // One document per wave (tokens [ds, de)): one buffer per stream over
+    // the document, a tile's loads at offsets from it (rows past the end
+    // read 0 and are masked), the document's constants once before its
+    // tiles and its score once after them.
+    constexpr int kCodeBytes = DOC == kDocInt4 ? 64 : 16;
+    const int ntok = (int)(de - ds);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.codes + ds * kCodeBytes, (uint32_t)ntok * kCodeBytes);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(RES ? p.rcodes + ds * 64 : p.codes, RES ? (uint32_t)ntok * 64u : 0u);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.tscale + ds, (uint32_t)ntok * 4u);
+    const __amdgpu_buffer_rsrc_t rsr = make_rsrc(RES ? p.rtscale + ds : p.tscale, RES ? (uint32_t)ntok * 4u : 0u);
+    {
+      const int64_t doc = targets[gw];
+      dscale = doc_scale ? doc_scale[doc] : p.scale;
+      if constexpr (RED == kRedLse) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale;
+      }
+    }
+    auto fetch = [&](int i, Tile& t) __attribute__((always_inline)) {
+      t.e = 0;
+      const int row = 16 * i + c;
+      if constexpr (DOC == kDocInt4)
+        t.a.w = load_b128(ra, row * 64 + 16 * g);
+      else
+        t.a.w = load_b32(ra, row * 16 + 4 * g);
+      if constexpr (RES) t.r.w = load_b128(rr, row * 64 + 16 * g);
+      if constexpr (!INTMAX) {
+        const v4u sv = load_b128(rs, (16 * i + 4 * g) * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t.s[q] = __uint_as_float(sv[q]);
+        if constexpr (RES) {
+          const v4u rv = load_b128(rsr, (16 * i + 4 * g) * 4);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) t.sr[q] = __uint_as_float(rv[q]);
+        }
+      }
+    };
+    auto meta = [&](int i, Pend&) { return max(0, min(16, ntok - 16 * i)); };
+    auto done = [&](Pend&, int) {};
+    run_ring(ntiles, fetch, meta, done);
+    len = ntok;
+    finish_target(t0);
+  } else if constexpr (NT > 2) {
+    // Eight row blocks: a tight loop over the table's tiles, one in flight.
+    Tile cur, nxt;
+    uint64_t e = tt[0];
+    load(e, cur);
+    for (int i = 0; i < ntiles; ++i) {
+      const uint64_t en = tt[i + 1];  // i + 1 <= ntiles: the table's padding entry last
+      load(en, nxt);
+      Acc a;
+      issue(a, cur);
+      Pend P = pend_of(cur);
+      const int rows = begin_tile(P);
+      consume_now(a, P, rows);
+      end_tile(P, rows);
+      cur = nxt;
+      e = en;
+    }
+  } else {
+    auto fetch = [&](int i, Tile& t) __attribute__((always_inline)) { load(entry(i), t); };
+    auto meta = [&](int, Pend& P) { return begin_tile(P); };
+    run_ring(ntiles, fetch, meta, end_tile);
   }
 }
 
