@@ -679,10 +679,20 @@ def bench_config5(args):
     def full():
         h.cascade_topk_async(dq, args.k, n, fs, fi, stream)
 
+    def recall(a, e):
+        return float(np.mean([len(set(a[i]) & set(e[i])) / args.k for i in range(b)]))
+
     wall, ev = _timed(step, args.steps, args.warmup, stream)
     full_wall, _ = _timed(full, args.steps, args.warmup, stream)
     got, exp = ti.cpu().numpy(), fi.cpu().numpy()
-    overlap = float(np.mean([len(set(got[i]) & set(exp[i])) / args.k for i in range(b)]))
+    overlap = recall(got, exp)
+    # The same cascade with the rescoring pass on the fp32 query (three int8
+    # limbs), against the fused scan of every document on the fp32 query.
+    h.set_rescore_limbs(3)
+    fp32_wall, _ = _timed(step, args.steps, args.warmup, stream)
+    fp32_full_wall, _ = _timed(full, args.steps, args.warmup, stream)
+    h.set_rescore_limbs(1)
+    got32, exp32 = ti.cpu().numpy(), fi.cpu().numpy()
     cpu = None
     if not args.no_cpu_baseline:
         # The same cascade on the C oracle over the first `sub` documents,
@@ -711,6 +721,9 @@ def bench_config5(args):
                    f"BASELINE config 5: {n} docs ({t} tokens) as 16 B signs + 4 B prefix scale + 64 B int4 residual + "
                    "4 B residual scale per token, query [4,32,128] int8, 512 candidates, top-10",
                    {"full_fused_scan_ms_per_step": full_wall, "top10_overlap_vs_full_fused_scan": overlap,
+                    "fp32_rescoring": {"ms_per_step": fp32_wall, "full_fused_scan_ms_per_step": fp32_full_wall,
+                                       "top10_recall_vs_fp32_full_fused_scan": recall(got32, exp32),
+                                       "int8_cascade_top10_recall_vs_fp32_full_fused_scan": recall(got, exp32)},
                     "bytes_per_token": 88, "cpu_baseline": cpu})
 
 

@@ -336,6 +336,14 @@ int msim_binary_set_residual(msim_binary_docs* h, const uint8_t* packed, int64_t
                              int64_t row_bytes, double scale, const float* token_scales,
                              int64_t count);
 int msim_binary_clear_residual(msim_binary_docs* h);
+/* No counterpart in the reference (its format has no binary prefix).  Query
+ * precision of the fused scoring (msim_binary_binres_score with fused = 1)
+ * and of a cascade's rescoring pass: limbs 1 (default) = the int8 query
+ * (v_mfma_i32_16x16x64_i8 on the int8 codes), 3 = the fp32 query as three
+ * int8 limbs (resolves q to 2^-24 of max|q|).  The coarse pass keeps the int8
+ * query.  Other values fail with MSIM_EINVAL. */
+int msim_binary_set_rescore_limbs(msim_binary_docs* h, int limbs);
+int msim_binary_get_rescore_limbs(const msim_binary_docs* h, int* limbs);
 /* Coarse (fused = 0) or fused (fused = 1) scores; candidates NULL (every
  * document, out [B, N]) or i64 [B, num_candidates] per batch row (out
  * [B, num_candidates]). */

@@ -498,6 +498,16 @@ class CudaPackedDocs:
     def clear_residual_int4(self):
         check(self._lib.msim_binary_clear_residual(self._h))
 
+    def set_rescore_limbs(self, limbs):
+        """Query limbs of fused scoring and cascade rescoring: 1 = int8 query,
+        3 = fp32 query (three int8 limbs)."""
+        check(self._lib.msim_binary_set_rescore_limbs(self._h, int(limbs)))
+
+    def get_rescore_limbs(self) -> int:
+        v = ctypes.c_int(0)
+        check(self._lib.msim_binary_get_rescore_limbs(self._h, ctypes.byref(v)))
+        return int(v.value)
+
     def binres_score_batch(self, query, fused=True, candidate_indices=None):
         """int8-query coarse (fused=False) or fused scores; candidate_indices
         None or i64 [B, M] per batch row."""

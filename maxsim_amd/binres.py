@@ -12,10 +12,13 @@ residual, cascade.py:60-93); this module defines it:
   dim 128.
 
 Queries are quantised to int8 per row (sigma = max|q| / 127, as the int4
-int8-query path).  Coarse similarity a_t (q . sign_t); fused similarity
-a_t (q . sign_t) + s^r_t (q . v^r_t); both reduced with MaxSim.  The
-cascade takes the coarse top-M per batch row, rescores them fused and
-returns the top-k (ties by document id), all on the GPU.
+int8-query path); the fused scores (and a cascade's rescoring) can instead
+take the fp32 query as three int8 limbs (query_precision="fp32").  Coarse
+similarity a_t (q . sign_t); fused similarity a_t (q . sign_t) +
+s^r_t (q . v^r_t), i.e. q . x'_t with x'_t = a_t sign_t + s^r_t v^r_t the
+reconstructed token; both reduced with MaxSim.  The cascade takes the
+coarse top-M per batch row, rescores them fused and returns the top-k (ties
+by document id), all on the GPU.
 """
 from __future__ import annotations
 
@@ -98,23 +101,51 @@ def _query(query_tokens, dim):
     return np.ascontiguousarray(q), squeeze
 
 
+_LIMBS = {"int8": 1, "fp32": 3}
+
+
+class _RescorePrecision:
+    """Sets the handle's rescoring query precision for one call."""
+
+    def __init__(self, handle, query_precision):
+        if query_precision not in _LIMBS:
+            raise ValueError("query_precision must be 'int8' or 'fp32'")
+        self.handle, self.limbs = handle, _LIMBS[query_precision]
+
+    def __enter__(self):
+        self.saved = self.handle.get_rescore_limbs()
+        self.handle.set_rescore_limbs(self.limbs)
+
+    def __exit__(self, *exc):
+        self.handle.set_rescore_limbs(self.saved)
+
+
 def binres_score(query_tokens, packed: BinaryResidualPackedDocs, *, fused: bool = True,
-                 candidate_indices=None) -> np.ndarray:
-    """Coarse (fused=False) or fused scores; candidate_indices None or i64 [B, M]."""
+                 candidate_indices=None, query_precision: str = "int8") -> np.ndarray:
+    """Coarse (fused=False) or fused scores; candidate_indices None or i64 [B, M].
+
+    query_precision: the query of the fused scores, "int8" (one int8 limb) or
+    "fp32" (three int8 limbs); the coarse scores always use the int8 query."""
     q, squeeze = _query(query_tokens, packed.dim)
     resident = binres_to_device(packed)
     cand = None if candidate_indices is None else np.asarray(candidate_indices, dtype=np.int64)
     if cand is not None and squeeze and cand.ndim == 1:
         cand = cand[np.newaxis]
-    out = resident.sign_data.binres_score_batch(q, fused=fused, candidate_indices=cand)
+    with _RescorePrecision(resident.sign_data, query_precision):
+        out = resident.sign_data.binres_score_batch(q, fused=fused, candidate_indices=cand)
     return out[0] if squeeze else out
 
 
-def binres_cascade_topk(query_tokens, packed: BinaryResidualPackedDocs, k: int, *, candidates: int):
-    """Coarse top-``candidates`` -> fused rescoring -> top-k, on the GPU."""
+def binres_cascade_topk(query_tokens, packed: BinaryResidualPackedDocs, k: int, *, candidates: int,
+                        query_precision: str = "int8"):
+    """Coarse top-``candidates`` -> fused rescoring -> top-k, on the GPU.
+
+    query_precision: the rescoring pass's query ("int8" or "fp32"); the coarse
+    pass uses the int8 query."""
     if k < 1 or k > candidates or candidates > packed.num_docs:
         raise ValueError("cascade sizes must satisfy 1 <= k <= candidates <= num_docs")
     q, squeeze = _query(query_tokens, packed.dim)
     resident = binres_to_device(packed)
-    scores, indices = resident.sign_data.cascade_topk(q, int(k), int(candidates))
+    with _RescorePrecision(resident.sign_data, query_precision):
+        scores, indices = resident.sign_data.cascade_topk(q, int(k), int(candidates))
     return (scores[0], indices[0]) if squeeze else (scores, indices)

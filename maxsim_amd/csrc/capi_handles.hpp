@@ -143,6 +143,9 @@ struct msim_binary_docs {
   double residual_scale = 1.0;
   int64_t max_doc_tiles = 1;  // 16-token tiles of the longest document
   msim::DeviceBuffer residual_packed, residual_token_scales16;
+  // Query limbs of the fused (prefix + residual) scoring and of a cascade's
+  // rescoring pass: 1 = the int8 query, 3 = the fp32 query (three int8 limbs).
+  int rescore_limbs = 1;
   // The int8-query scan over the sign stream (a cascade's prefix pass): its
   // tables (cached by wave count) and whether every token scale suits its
   // one-fma epilogue ([kScanFmaMinScale, kScanFmaMaxScale)).

@@ -944,7 +944,7 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
   const DocStreams prefix = binres_streams(h, false), fused = binres_streams(h, true);
   QueryInput qi;
   qi.d_query = d_query;
-  qi.limbs = 1;
+  qi.limbs = h->rescore_limbs;
   if (m == h->num_docs) {
     h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
     run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, kRedMax, 1.0f, batch, query_tokens, nullptr,
@@ -954,13 +954,22 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
               "launch topk selection kernel");
     return;
   }
-  // One quantisation for both passes: the prefix pass's sign layout, and the
-  // int4 layout the fused pass reads (its sign stream is unpacked in the int4
-  // lane order).
+  // With the int8 query, one quantisation serves both passes: the prefix
+  // pass's sign layout, and the int4 layout the fused pass reads (its sign
+  // stream is unpacked in the int4 lane order).  With the fp32 query, the
+  // rescoring pass quantises its three limbs itself (its buffers sized first,
+  // so that no buffer the prefix pass reads is reallocated while in flight).
   QueryInput coarse_q = qi;
+  coarse_q.limbs = 1;
   coarse_q.alt_int4 = true;
   QueryInput fine_q = qi;
-  fine_q.from_alt = true;
+  if (qi.limbs == 1) {
+    fine_q.from_alt = true;
+  } else {
+    const int64_t rows_padded = ceil_div(batch * query_tokens, 16) * 16 + 128;
+    h->ws.qpack.ensure((size_t)qi.limbs * rows_padded * 128, "hipMalloc query limbs");
+    h->ws.qsum.ensure(sizeof(int32_t) * qi.limbs * rows_padded, "hipMalloc query limb sums");
+  }
   cascade_device(
       h->ws, batch, h->num_docs, k, m,
       [&](float* d) {
@@ -1006,6 +1015,22 @@ extern "C" int msim_binary_set_residual(msim_binary_docs* h, const uint8_t* pack
   });
 }
 
+extern "C" int msim_binary_set_rescore_limbs(msim_binary_docs* h, int limbs) {
+  return guarded([&] {
+    require_handle(h);
+    if (limbs != 1 && limbs != 3) throw InvalidArgument("rescore limbs must be 1 (int8 query) or 3 (fp32 query)");
+    h->rescore_limbs = limbs;
+  });
+}
+
+extern "C" int msim_binary_get_rescore_limbs(const msim_binary_docs* h, int* limbs) {
+  return guarded([&] {
+    require_handle(h);
+    if (limbs == nullptr) throw InvalidArgument("limbs must not be null");
+    *limbs = h->rescore_limbs;
+  });
+}
+
 extern "C" int msim_binary_clear_residual(msim_binary_docs* h) {
   return guarded([&] {
     require_handle(h);
@@ -1029,7 +1054,7 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
     select_device(h->device);
     QueryInput qi;
     qi.d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
-    qi.limbs = 1;
+    qi.limbs = fused ? h->rescore_limbs : 1;
     Targets t{candidates, num_candidates, candidates != nullptr};
     h->scores.ensure(sizeof(float) * batch * targets, "hipMalloc score cache");
     // Prefix scores of every document: the scan a cascade's prefix pass uses.

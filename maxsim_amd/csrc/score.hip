@@ -808,6 +808,7 @@ hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, i
   if (doc == kDocSign && !residual && limbs == 3) { MSIM_SCORE_NT(kDocSign, false, 3); }
   if (doc == kDocSign && !residual && limbs == 1) { MSIM_SCORE_NT(kDocSign, false, 1); }
   if (doc == kDocSign && residual && limbs == 1) { MSIM_SCORE_NT(kDocSign, true, 1); }
+  if (doc == kDocSign && residual && limbs == 3) { MSIM_SCORE_NT(kDocSign, true, 3); }
 #undef MSIM_SCORE_NT
   return hipErrorInvalidValue;
 }

@@ -168,6 +168,76 @@ def test_binres_cascade_equals_host_procedure(gpu, prefix_scan, mode):
     assert overlap >= 0.9
 
 
+def _binres_recon(oracle, docs):
+    """Reconstructed tokens a_t sign_t + s^r_t v^r_t (the oracle's packing):
+    the fused similarity is q . x'_t, so the fp32-query fused scores are the
+    dense MaxSim over them."""
+    signs, a, _, rv, rs = oracle.pack_binary_residual(docs)
+    sign = np.where(np.asarray(docs) >= 0, 1.0, -1.0)
+    return (a[:, None].astype(np.float64) * sign + rs[:, None].astype(np.float64) * rv).astype(np.float32)
+
+
+def test_binres_fp32_fused_scores_match_dense_oracle(gpu, oracle):
+    """Fused scores with the fp32 query (three int8 limbs) against the dense
+    MaxSim over the reconstructed tokens, at the fp32 bar (rtol 1e-5); the
+    int8-query scores differ from it by the query rounding."""
+    from maxsim_amd.binres import binres_score
+
+    docs, offsets = ragged_fixture(150, 44, lo=1, hi=50)
+    query = np.random.default_rng(45).standard_normal((3, 9, 128)).astype(np.float32)
+    packed = _binres(docs, offsets)
+    recon = _binres_recon(oracle, docs)
+    exp = oracle.dense_scores(query, recon, offsets)
+    got = binres_score(query, packed, fused=True, query_precision="fp32")
+    _close(got, exp, 1e-5)
+    assert np.max(np.abs(binres_score(query, packed, fused=True) - exp)) > np.max(np.abs(got - exp))
+    cand = np.random.default_rng(46).integers(0, 150, size=(3, 20)).astype(np.int64)
+    got_c = binres_score(query, packed, fused=True, candidate_indices=cand, query_precision="fp32")
+    np.testing.assert_array_equal(got_c, np.take_along_axis(got, cand, axis=1))
+    # the setting is per call: the handle is back on the int8 query
+    assert packed.sign_data.get_rescore_limbs() == 1
+
+
+@pytest.mark.parametrize("qt", [32, 64])
+def test_binres_cascade_fp32_rescoring_equals_host_procedure(gpu, qt):
+    """int8-query coarse pass -> top-M -> fp32-query rescoring -> top-k equals
+    the same steps through the scoring calls; with every document a candidate
+    it is the fp32 fused top-k."""
+    from maxsim_amd import synthetic
+    from maxsim_amd.binres import binres_cascade_topk, binres_score
+
+    corpus = synthetic.make_corpus(400, 64, 192, seed=48)
+    query = synthetic.make_queries(corpus, 3)
+    if qt != query.shape[1]:
+        query = np.random.default_rng(qt).standard_normal((3, qt, 128)).astype(np.float32)
+    packed = _binres(corpus.embeddings, corpus.offsets)
+    k, m = 10, 96
+    top_s, top_i = binres_cascade_topk(query, packed, k, candidates=m, query_precision="fp32")
+    coarse = binres_score(query, packed, fused=False)
+    cands = np.stack([_stable(coarse[b], m) for b in range(3)])
+    fine = binres_score(query, packed, fused=True, candidate_indices=cands, query_precision="fp32")
+    for b in range(3):
+        order = _stable(fine[b], k, tie_ids=cands[b])
+        np.testing.assert_array_equal(top_i[b], cands[b][order])
+        np.testing.assert_array_equal(top_s[b], fine[b][order])
+    full = binres_score(query, packed, fused=True, query_precision="fp32")
+    fs, fi = binres_cascade_topk(query, packed, k, candidates=400, query_precision="fp32")
+    for b in range(3):
+        np.testing.assert_array_equal(fi[b], _stable(full[b], k))
+        np.testing.assert_array_equal(fs[b], full[b][fi[b]])
+
+
+def test_binres_rescore_limbs_validation(gpu):
+    docs, offsets = ragged_fixture(20, 3, lo=1, hi=20)
+    h = _binres(docs, offsets).sign_data
+    for bad in (0, 2, 4):
+        with pytest.raises(ValueError):
+            h.set_rescore_limbs(bad)
+    h.set_rescore_limbs(3)
+    assert h.get_rescore_limbs() == 3
+    h.set_rescore_limbs(1)
+
+
 # ------------------------------------------------------------- public API
 
 
