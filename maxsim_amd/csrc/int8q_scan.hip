@@ -544,18 +544,27 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (blockIdx.x == 0) tail_block_ranges(p.block_pos, (int)gridDim.x, bs, blen);
   group_sync_lds();
   if ((int)threadIdx.x < p.batch) {
-    uint64_t a0 = 0, a1 = 0, a2 = 0;
+    // The waves' sorted top threes merged as a tree: the i-th largest of two
+    // sorted lists x, y is the maximum over j of min(x[j - 1], y[i - j - 1])
+    // (x[-1] = y[-1] = +inf), so the top three of x and y are
+    // max(x0, y0), max(x1, y1, min(x0, y0)), max(x2, y2, min(x1, y0), min(x0, y1)).
+    struct Top3 {
+      uint64_t k0, k1, k2;
+    };
+    auto merge3 = [](const Top3& x, const Top3& y) {
+      Top3 z;
+      z.k0 = max(x.k0, y.k0);
+      z.k1 = max(max(x.k1, y.k1), min(x.k0, y.k0));
+      z.k2 = max(max(x.k2, y.k2), max(min(x.k1, y.k0), min(x.k0, y.k1)));
+      return z;
+    };
+    static_assert(kScanWaves == 4, "two merge levels");
+    Top3 t[kScanWaves];
 #pragma unroll
-    for (int w = 0; w < kScanWaves; ++w) {
-#pragma unroll
-      for (int i = 0; i < 3; ++i) {
-        const uint64_t key = s_top[w][threadIdx.x][i];
-        const uint64_t m0 = min(a0, key), m1 = min(a1, m0);
-        a0 = max(a0, key);
-        a1 = max(a1, m0);
-        a2 = max(a2, m1);
-      }
-    }
+    for (int w = 0; w < kScanWaves; ++w)
+      t[w] = {s_top[w][threadIdx.x][0], s_top[w][threadIdx.x][1], s_top[w][threadIdx.x][2]};
+    const Top3 all = merge3(merge3(t[0], t[1]), merge3(t[2], t[3]));
+    const uint64_t a0 = all.k0, a1 = all.k1, a2 = all.k2;
     const uint64_t ktag = tail_key_tag(tag);
     uint64_t* rec = p.tail_rec + (int64_t)threadIdx.x * 3 * kScanTailBlocks + blockIdx.x;
     __hip_atomic_store(rec, a0 != 0 ? a0 : ktag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
