@@ -142,8 +142,10 @@ def test_binres_prefix_scan_is_bit_exact(gpu, oracle, prefix_scan, shape):
     _close(binres_score(query, packed, fused=False), exp, 1e-6)
 
 
-@pytest.mark.parametrize("mode", [1, 0])
-def test_binres_cascade_equals_host_procedure(gpu, prefix_scan, mode):
+@pytest.mark.parametrize("mode,qt", [(1, 32), (0, 32), (1, 64)])
+def test_binres_cascade_equals_host_procedure(gpu, prefix_scan, mode, qt):
+    """qt = 64: passes of 64 query rows (eight row blocks) in the rescoring
+    pass's one-document-per-wave form."""
     from maxsim_amd import synthetic
     from maxsim_amd.binres import binres_cascade_topk, binres_score
 
@@ -151,6 +153,8 @@ def test_binres_cascade_equals_host_procedure(gpu, prefix_scan, mode):
 
     corpus = synthetic.make_corpus(400, 64, 192, seed=47)
     query = synthetic.make_queries(corpus, 4)
+    if qt != query.shape[1]:
+        query = np.concatenate([query, query[:, ::-1] * np.float32(0.5)], axis=1)
     packed = _binres(corpus.embeddings, corpus.offsets)
     k, m = 10, 128
     top_s, top_i = binres_cascade_topk(query, packed, k, candidates=m)
