@@ -310,6 +310,11 @@ def bench_config2(args):
         handle._h, batch, qtok, ptr(scores), sptr)))
     assert np.array_equal(scores.cpu().numpy(), ref_scores), "scan scores differ between entry points"
 
+    # The dispatch floor: a one-workgroup kernel (torch's fill of one
+    # element) launched back to back on the same stream, timed the same way.
+    one = torch.empty(1, dtype=torch.float32, device=dev)
+    floor_ms = block_times(lambda: one.fill_(0.0))
+
     # the scan's workgroups: eight waves per CU (four per workgroup), at most one wave per document
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     nbytes = algorithmic_bytes(num_tokens, num_docs, batch, qtok, k, -(-min(cus * 8, num_docs) // 4))
@@ -430,6 +435,10 @@ def bench_config2(args):
             "scoring_only_ms_avg": float(score_ms.mean()),
             "scoring_only_frac": (nbytes["total"] - 4 * batch * num_docs - 12 * batch * k)
                                  / (float(score_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "dispatch_floor_ms": float(np.median(floor_ms)),
+            "frac_excluding_dispatch_floor": nbytes["total"]
+                                             / ((float(scan_ms.mean()) - float(np.median(floor_ms))) * 1e-3)
+                                             / 1e9 / HBM_PEAK_GBS,
             "cold_kernel_ms_avg": None if cold_scan_ms is None else float(cold_scan_ms.mean()),
             "cold_frac": None if cold_scan_ms is None
                          else nbytes["total"] / (float(cold_scan_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
