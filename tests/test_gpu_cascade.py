@@ -91,6 +91,33 @@ def test_cascade_tie_order_by_document_id(gpu):
     np.testing.assert_array_equal(idx, [0, 1, 2])
 
 
+def test_cascade_many_ties_at_the_candidate_threshold(gpu):
+    """3,000 documents that are 12 distinct ones repeated (ties in whole
+    groups of 250), 512 candidates: the threshold falls inside a group, so the
+    selector must keep that group's lowest ids (the radix rounds reach the
+    position bits).  Equal to the host procedure on the device's scores."""
+    from maxsim_amd.cascade import cascade_topk, pack_residual_int4, prefix_score, residual_int4_to_device, \
+        residual_score
+
+    rng = np.random.default_rng(44)
+    distinct = [rng.standard_normal((int(rng.integers(3, 40)), 128)).astype(np.float32) for _ in range(12)]
+    order = np.repeat(np.arange(12), 250)
+    rng.shuffle(order)
+    docs = np.concatenate([distinct[i] for i in order])
+    offsets = np.concatenate([[0], np.cumsum([distinct[i].shape[0] for i in order])]).astype(np.int64)
+    packed = residual_int4_to_device(pack_residual_int4(docs, offsets))
+    query = rng.standard_normal((2, 8, 128)).astype(np.float32)
+    k, m = 10, 512
+    ts, ti = cascade_topk(query, packed, k, candidates=m)
+    coarse = prefix_score(query, packed)
+    for b in range(2):
+        cands = np.sort(_stable(coarse[b], m))
+        fine = residual_score(query[b], packed, candidate_indices=cands)
+        top = _stable(fine, k, tie_ids=cands)
+        np.testing.assert_array_equal(ti[b], cands[top])
+        np.testing.assert_array_equal(ts[b], fine[top])
+
+
 # --------------------------------------------------- binary prefix + residual
 
 
