@@ -37,6 +37,19 @@ void DeviceBuffer::ensure(size_t bytes, const char* what) {
   cap = bytes;
 }
 
+HostBuffer::~HostBuffer() {
+  if (ptr) (void)hipHostFree(ptr);
+}
+
+void HostBuffer::ensure(size_t bytes, const char* what) {
+  if (bytes <= cap) return;
+  void* next = nullptr;
+  check_hip(hipHostMalloc(&next, bytes, hipHostMallocCoherent), what);
+  if (ptr) (void)hipHostFree(ptr);
+  ptr = next;
+  cap = bytes;
+}
+
 void DeviceBuffer::reset() {
   if (ptr) (void)hipFree(ptr);
   ptr = nullptr;
@@ -566,15 +579,22 @@ extern "C" int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query,
     if (batch == 0) return;
     select_device(h->device);
     hipStream_t stream = nullptr;
-    float* d_query = upload_query(h, query, batch, query_tokens, dim, stream);
+    // The query, the top scores and the top ids share one pinned buffer: the
+    // quantisation kernel reads the query from it and the selection writes
+    // its results into it.
+    const size_t qbytes = sizeof(float) * (size_t)(batch * query_tokens * dim);
+    const size_t sbytes = sizeof(float) * (size_t)(batch * k), ibytes = sizeof(int64_t) * (size_t)(batch * k);
+    const size_t q_al = (qbytes + 255) & ~(size_t)255, s_al = (sbytes + 255) & ~(size_t)255;
+    h->host_io.ensure(q_al + s_al + ibytes, "hipHostMalloc int8q query and result staging");
+    char* io = h->host_io.as<char>();
+    std::memcpy(io, query, qbytes);
+    float* h_top_s = reinterpret_cast<float*>(io + q_al);
+    int64_t* h_top_i = reinterpret_cast<int64_t*>(io + q_al + s_al);
     float* d_scores = ensure_scores(h, batch, h->num_docs);
-    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc int8q top score cache");
-    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc int8q top index cache");
-    search_int8q(h, d_query, batch, query_tokens, d_scores, k, h->top_scores.as<float>(),
-                 h->top_indices.as<int64_t>(), stream);
-    check_hip(hipMemcpyAsync(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top scores to host");
-    check_hip(hipMemcpyAsync(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost, stream), "copy int8q top indices to host");
+    search_int8q(h, reinterpret_cast<const float*>(io), batch, query_tokens, d_scores, k, h_top_s, h_top_i, stream);
     check_hip(hipStreamSynchronize(stream), "synchronize int8q topk kernels");
+    std::memcpy(out_scores, h_top_s, sbytes);
+    std::memcpy(out_indices, h_top_i, ibytes);
   });
 }
 

@@ -11,7 +11,7 @@ namespace msim {
 // Device workspaces of one handle's generalized scoring calls (grow
 // monotonically, freed with the handle; cu:3057-3067).
 struct ScoreWorkspace {
-  DeviceBuffer qpack, colmul, qsum, weights, pooled, query, qbits;
+  DeviceBuffer qpack, colmul, qsum, weights, pooled, qbits;
   DeviceBuffer qpack_alt;  // the query also in the int4 layout (QueryInput::alt_int4)
   std::vector<float> weights_host;  // what `weights` holds (a repeated weight vector is not copied again)
   DeviceBuffer full_info, full_tiles;  // cached whole-corpus tables
@@ -20,8 +20,11 @@ struct ScoreWorkspace {
   DeviceBuffer cand_ids, cand_info, cand_tiles;
   // cascade: coarse scores, top-M candidates (scores / ids), fine scores
   DeviceBuffer coarse, top_m_scores, top_m_ids, fine;
+  // Synchronous calls: the fp32 query and the top-k results, in pinned host
+  // memory that the kernels read and write directly.
+  HostBuffer host_query, host_out;
   uint64_t bytes() const {
-    return qpack.cap + qpack_alt.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + query.cap + qbits.cap + full_info.cap +
+    return qpack.cap + qpack_alt.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + qbits.cap + full_info.cap +
            full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap + coarse.cap + top_m_scores.cap +
            top_m_ids.cap + fine.cap;
   }
@@ -29,7 +32,7 @@ struct ScoreWorkspace {
 
 // Which query the generalized path scores.
 struct QueryInput {
-  const float* d_query = nullptr;    // fp32 [rows, 128] on the device, or
+  const float* d_query = nullptr;    // fp32 [rows, 128] (device or pinned host memory), or
   const uint8_t* d_qbits = nullptr;  // sign bits [rows, 16] (pack_signs order)
   int limbs = 3;                     // 3: fp32 split into int8 limbs, 1: int8
   bool recip = false;                // int8 rounding q * (1 / sigma) (binary int8q)
@@ -111,7 +114,8 @@ struct msim_int4_docs {
   // per-token 1/16 when the corpus has no token scales.
   msim::DeviceBuffer codes128, residual128, ones16;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
-  msim::DeviceBuffer query, qpack, qscale, qbias, scores, top_scores, top_indices, rowmax;
+  msim::DeviceBuffer query, qpack, qscale, qbias, scores, rowmax;
+  msim::HostBuffer host_io;  // synchronous top-k: query in, results out (pinned)
   // Scan with fused top-k: launch counter, key rows of kScanTailRow tagged
   // 64-bit keys and workgroup records (3 x kScanTailBlocks tagged words per row).
   msim::DeviceBuffer tail_epoch, tail_keys, tail_rec;
@@ -122,7 +126,7 @@ struct msim_int4_docs {
            residual_token_scales16.cap + codes128.cap + residual128.cap + ones16.cap;
   }
   uint64_t workspace_bytes() const {
-    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap + top_scores.cap + top_indices.cap +
+    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap +
            rowmax.cap + wave_info.cap + tile_table.cap + tail_epoch.cap + tail_keys.cap + tail_rec.cap + ws.bytes();
   }
 };
@@ -152,7 +156,7 @@ struct msim_binary_docs {
   bool token_scales_fma = false;
   int64_t scan_partition_waves = 0, num_scan_waves = 0, scan_tile_stride = 0;
   msim::DeviceBuffer scan_wave_info, scan_tile_table;
-  msim::DeviceBuffer scores, top_scores, top_indices, iscores;
+  msim::DeviceBuffer scores, iscores;
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {
@@ -160,7 +164,7 @@ struct msim_binary_docs {
            residual_token_scales16.cap;
   }
   uint64_t workspace_bytes() const {
-    return scores.cap + top_scores.cap + top_indices.cap + iscores.cap + scale_override.cap + scan_wave_info.cap +
+    return scores.cap + iscores.cap + scale_override.cap + scan_wave_info.cap +
            scan_tile_table.cap + ws.bytes();
   }
 };

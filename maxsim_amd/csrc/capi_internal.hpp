@@ -85,6 +85,24 @@ struct DeviceBuffer {
   }
 };
 
+// Pinned, coherent host memory that only grows.  The synchronous top-k entry
+// points stage the query and the results there: the kernels read the query
+// and write the results across the host link themselves, so a call makes no
+// staging copies of its own.
+struct HostBuffer {
+  void* ptr = nullptr;
+  size_t cap = 0;
+  HostBuffer() = default;
+  HostBuffer(const HostBuffer&) = delete;
+  HostBuffer& operator=(const HostBuffer&) = delete;
+  ~HostBuffer();
+  void ensure(size_t bytes, const char* what);
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
 // util.hip
 hipError_t launch_fill_f32(float* d, int64_t n, float value, hipStream_t stream);
 

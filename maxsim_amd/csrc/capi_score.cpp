@@ -286,20 +286,45 @@ void check_k(int64_t k, int64_t n) {
 }
 
 // fp32 query [B, Q, dim] (host) -> device [B * Q, 128], zero-padded dims.
-const float* upload_query128(ScoreWorkspace& ws, const float* query, int64_t rows, int64_t dim) {
+// The fp32 query of a synchronous call as [rows, 128] (zero-padded from dim)
+// in the workspace's pinned host buffer: the quantisation kernels read it
+// there, so no staging copy is queued.
+const float* stage_query128(ScoreWorkspace& ws, const float* query, int64_t rows, int64_t dim) {
   const size_t bytes = sizeof(float) * (size_t)std::max<int64_t>(rows, 1) * 128;
-  ws.query.ensure(bytes, "hipMalloc query cache");
-  if (rows == 0) return ws.query.as<float>();
+  ws.host_query.ensure(bytes, "hipHostMalloc query staging");
+  float* q = ws.host_query.as<float>();
+  if (rows == 0) return q;
   if (dim == 128) {
-    check_hip(hipMemcpy(ws.query.ptr, query, sizeof(float) * rows * 128, hipMemcpyHostToDevice), "copy query to device");
+    std::memcpy(q, query, sizeof(float) * (size_t)rows * 128);
   } else {
-    std::vector<float> wide((size_t)rows * 128, 0.0f);
-    for (int64_t r = 0; r < rows; ++r) std::memcpy(&wide[r * 128], query + r * dim, sizeof(float) * dim);
-    check_hip(hipMemcpy(ws.query.ptr, wide.data(), wide.size() * sizeof(float), hipMemcpyHostToDevice),
-              "copy query to device");
+    for (int64_t r = 0; r < rows; ++r) {
+      std::memcpy(q + r * 128, query + r * dim, sizeof(float) * (size_t)dim);
+      std::memset(q + r * 128 + dim, 0, sizeof(float) * (size_t)(128 - dim));
+    }
   }
-  return ws.query.as<float>();
+  return q;
 }
+
+// Top-k results of a synchronous call: the selection kernel writes them into
+// the workspace's pinned host buffer; finish() waits for the stream and
+// copies them out.
+struct HostTopk {
+  float* s = nullptr;
+  int64_t* i = nullptr;
+  size_t sbytes = 0, ibytes = 0;
+  HostTopk(ScoreWorkspace& ws, int64_t batch, int64_t k)
+      : sbytes(sizeof(float) * (size_t)(batch * k)), ibytes(sizeof(int64_t) * (size_t)(batch * k)) {
+    const size_t s_al = (sbytes + 255) & ~(size_t)255;
+    ws.host_out.ensure(std::max<size_t>(s_al + ibytes, 8), "hipHostMalloc top-k result staging");
+    s = ws.host_out.as<float>();
+    i = reinterpret_cast<int64_t*>(ws.host_out.as<char>() + s_al);
+  }
+  void finish(float* out_s, int64_t* out_i, hipStream_t stream) const {
+    check_hip(hipStreamSynchronize(stream), "synchronize top-k selection");
+    std::memcpy(out_s, s, sbytes);
+    std::memcpy(out_i, i, ibytes);
+  }
+};
 
 // ------------------------------------------------------------------ int4
 
@@ -338,7 +363,7 @@ float* int4_score_device(msim_int4_docs* h, const float* query, int64_t batch, i
                          int64_t m, bool residual, hipStream_t stream) {
   const int64_t targets = cand ? m : h->num_docs;
   const DocStreams s = int4_streams(h, residual);
-  const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+  const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
   h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
   QueryInput qi;
   qi.d_query = d_query;
@@ -374,15 +399,10 @@ extern "C" int msim_int4_topk_batch(msim_int4_docs* h, const float* query, int64
     if (batch == 0) return;
     select_device(h->device);
     float* d = int4_score_device(h, query, batch, query_tokens, dim, kRedMax, {}, 1.0f, nullptr, 0, false, nullptr);
-    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
-    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
-    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
-                          h->top_indices.as<int64_t>(), nullptr),
+    const HostTopk out(h->ws, batch, k);
+    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, out.s, out.i, nullptr),
               "launch topk selection kernel");
-    check_hip(hipMemcpy(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost),
-              "copy top scores to host");
-    check_hip(hipMemcpy(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost),
-              "copy top indices to host");
+    out.finish(out_scores, out_indices, nullptr);
   });
 }
 
@@ -440,7 +460,7 @@ float* binary_score_device(msim_binary_docs* h, const float* query, int64_t batc
                            int64_t dim, int limbs, bool recip, const DocStreams& s, int reducer,
                            const std::vector<float>& w, float temperature, const int64_t* cand, int64_t m) {
   const int64_t targets = cand ? m : h->num_docs;
-  const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+  const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
   h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
   QueryInput qi;
   qi.d_query = d_query;
@@ -454,15 +474,10 @@ float* binary_score_device(msim_binary_docs* h, const float* query, int64_t batc
 
 void copy_topk_out(msim_binary_docs* h, const float* d_scores, int64_t batch, int64_t k, float* out_scores,
                    int64_t* out_indices, hipStream_t stream) {
-  h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
-  h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
-  check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
-                        h->top_indices.as<int64_t>(), stream),
+  const HostTopk out(h->ws, batch, k);
+  check_hip(launch_topk(d_scores, batch, h->num_docs, h->num_docs, k, nullptr, out.s, out.i, stream),
             "launch topk selection kernel");
-  check_hip(hipMemcpy(out_scores, h->top_scores.ptr, sizeof(float) * batch * k, hipMemcpyDeviceToHost),
-            "copy top scores to host");
-  check_hip(hipMemcpy(out_indices, h->top_indices.ptr, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost),
-            "copy top indices to host");
+  out.finish(out_scores, out_indices, stream);
 }
 
 void check_binary_query(const msim_binary_docs* h, int64_t batch, int64_t query_tokens, int64_t dim) {
@@ -789,11 +804,6 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
             "launch cascade final selection");
 }
 
-void copy_topk_host(const float* d_s, const int64_t* d_i, int64_t batch, int64_t k, float* out_s, int64_t* out_i) {
-  check_hip(hipMemcpy(out_s, d_s, sizeof(float) * batch * k, hipMemcpyDeviceToHost), "copy top scores to host");
-  check_hip(hipMemcpy(out_i, d_i, sizeof(int64_t) * batch * k, hipMemcpyDeviceToHost), "copy top indices to host");
-}
-
 }  // namespace
 
 extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
@@ -816,18 +826,17 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
     select_device(h->device);
     const DocStreams prefix = int4_streams(h, false), fused = int4_streams(h, true);
     QueryInput qi;
-    qi.d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
     qi.limbs = 3;
     const float* wp = w.empty() ? nullptr : w.data();
-    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
-    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
+    const HostTopk out(h->ws, batch, k);
     if (candidates == h->num_docs) {
       // Every document is a candidate: full fused scoring (cascade.py:342-351).
       h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
       run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, qi, red, (float)temperature, batch,
                         query_tokens, wp, Targets{}, h->scores.as<float>(), h->num_docs, nullptr, nullptr);
-      check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr,
-                            h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr),
+      check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr, out.s, out.i,
+                            nullptr),
                 "launch topk selection kernel");
     } else {
       cascade_device(
@@ -849,10 +858,10 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, again, red, (float)temperature, batch,
                               query_tokens, wp, t, d, candidates, nullptr, nullptr);
           },
-          h->top_scores.as<float>(), h->top_indices.as<int64_t>(), nullptr,
-          candidate_layout(batch, query_tokens, qi.limbs, candidates, h->max_doc_tiles), h->offsets.as<int64_t>());
+          out.s, out.i, nullptr, candidate_layout(batch, query_tokens, qi.limbs, candidates, h->max_doc_tiles),
+          h->offsets.as<int64_t>());
     }
-    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+    out.finish(out_scores, out_indices, nullptr);
   });
 }
 
@@ -1053,7 +1062,7 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
     if (batch == 0 || targets == 0) return;
     select_device(h->device);
     QueryInput qi;
-    qi.d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
+    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
     qi.limbs = fused ? h->rescore_limbs : 1;
     Targets t{candidates, num_candidates, candidates != nullptr};
     h->scores.ensure(sizeof(float) * batch * targets, "hipMalloc score cache");
@@ -1078,12 +1087,10 @@ extern "C" int msim_binary_cascade_topk(msim_binary_docs* h, const float* query,
     binres_streams(h, true);
     if (batch == 0) return;
     select_device(h->device);
-    const float* d_query = upload_query128(h->ws, query, batch * query_tokens, dim);
-    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
-    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
-    binres_cascade(h, d_query, batch, query_tokens, k, candidates, h->top_scores.as<float>(),
-                   h->top_indices.as<int64_t>(), nullptr);
-    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+    const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    const HostTopk out(h->ws, batch, k);
+    binres_cascade(h, d_query, batch, query_tokens, k, candidates, out.s, out.i, nullptr);
+    out.finish(out_scores, out_indices, nullptr);
   });
 }
 
@@ -1147,12 +1154,10 @@ extern "C" int msim_int4_topk_score(msim_int4_docs* h, const float* query, int64
     select_device(h->device);
     float* d = int4_score_device(h, query, batch, query_tokens, dim, red, w, (float)temperature, nullptr, 0,
                                  residual != 0, nullptr);
-    h->top_scores.ensure(sizeof(float) * batch * k, "hipMalloc top score cache");
-    h->top_indices.ensure(sizeof(int64_t) * batch * k, "hipMalloc top index cache");
-    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, h->top_scores.as<float>(),
-                          h->top_indices.as<int64_t>(), nullptr),
+    const HostTopk out(h->ws, batch, k);
+    check_hip(launch_topk(d, batch, h->num_docs, h->num_docs, k, nullptr, out.s, out.i, nullptr),
               "launch topk selection kernel");
-    copy_topk_host(h->top_scores.as<float>(), h->top_indices.as<int64_t>(), batch, k, out_scores, out_indices);
+    out.finish(out_scores, out_indices, nullptr);
   });
 }
 

@@ -357,9 +357,10 @@ def _dedupe_candidate_ids(candidate_ids) -> tuple[str, ...]:
 def _format_topk_results(scores, indices, doc_ids):
     s = np.asarray(scores, dtype=np.float32)
     i = np.asarray(indices, dtype=np.int64)
+    # Python floats and ints once per array (tolist), not per numpy scalar.
     if s.ndim == 1:
-        return _format_result_row(s, i, doc_ids)
-    return [_format_result_row(rs, ri, doc_ids) for rs, ri in zip(s, i)]
+        return _format_result_row(s.tolist(), i.tolist(), doc_ids)
+    return [_format_result_row(rs, ri, doc_ids) for rs, ri in zip(s.tolist(), i.tolist())]
 
 
 def _format_candidate_results(scores, candidate_indices, candidate_ids, k: int):
@@ -377,5 +378,4 @@ def _format_candidate_row(scores, candidate_indices, candidate_ids, k: int):
 
 
 def _format_result_row(scores, indices, doc_ids):
-    return [SearchResult(doc_id=doc_ids[int(i)], score=float(s), rank=r)
-            for r, (s, i) in enumerate(zip(scores, indices), start=1)]
+    return [SearchResult(doc_ids[i], s, r) for r, (s, i) in enumerate(zip(scores, indices), start=1)]

@@ -67,6 +67,26 @@ def test_int8q_topk_matches_stable_order(gpu, oracle, granularity):
     np.testing.assert_array_equal(top_scores, ref_scores)
 
 
+def test_int8q_topk_consecutive_calls_see_their_own_query(gpu, oracle):
+    """The synchronous top-k stages the query and its results in one pinned
+    host buffer per handle that the kernels read and write directly: calls in
+    a row, with different queries, shapes and k (the buffer grows, then is
+    reused by a smaller call), each return the oracle's answer for their own
+    query."""
+    docs, offsets = ragged_fixture(300, seed=31)
+    packed = pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    device = int4_to_device(packed)
+    rng = np.random.default_rng(37)
+    queries = [rng.standard_normal(s).astype(np.float32) for s in [(2, 8, 128), (4, 32, 128), (1, 3, 128)]]
+    for i, (query, k) in enumerate([(queries[0], 5), (queries[1], 10), (queries[0], 5), (queries[2], 32),
+                                    (queries[1], 1)]):
+        print(f"call {i}: query {query.shape} k={k}", flush=True)
+        top_scores, top_ids = device.data.topk_batch_int8q(query, k)
+        ref_scores, ref_ids = oracle.topk(_scores(oracle, packed, query), k)
+        np.testing.assert_array_equal(top_ids, ref_ids)
+        np.testing.assert_array_equal(top_scores, ref_scores)
+
+
 def test_topk_ties_prefer_lower_doc_id(gpu):
     """Equal documents tie; the lower id wins (tests/test_int4_reference.py:129-146)."""
     docs = np.array([[1] * 128, [1] * 128, [-1] * 128, [1] * 128], np.float32)
