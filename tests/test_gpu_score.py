@@ -148,6 +148,27 @@ def test_int4_fp32_topk_is_stable_order(gpu, oracle):
         np.testing.assert_array_equal(si, row[order])
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_int4_fp32_topk_consecutive_calls(gpu, oracle, dim):
+    """Synchronous top-k calls stage their query (widened to 128 dims) and
+    their results in the handle's pinned host buffers: calls in a row with
+    other queries, shapes and k each match the device's own full scores."""
+    docs, offsets = ragged_fixture(200, 15, lo=1, hi=30, dim=dim)
+    packed, h = _int4_handle(docs, offsets, "token")
+    rng = np.random.default_rng(16)
+    queries = [rng.standard_normal(s + (dim,)).astype(np.float32) for s in [(3, 7), (1, 40), (2, 2)]]
+    for i, (query, k) in enumerate([(queries[0], 10), (queries[1], 3), (queries[0], 10), (queries[2], 25)]):
+        print(f"call {i}: query {query.shape} k={k}", flush=True)
+        scores = h.maxsim_batch(query)
+        _close(scores, oracle.int4_fp32_scores(query, packed.values, offsets, scale=packed.scale,
+                                               token_scale=packed.token_scale))
+        top_s, top_i = h.topk_batch(query, k)
+        for row, si, ii in zip(scores, top_s, top_i):
+            order = np.lexsort((np.arange(row.shape[0]), -row))[:k]
+            np.testing.assert_array_equal(ii, order)
+            np.testing.assert_array_equal(si, row[order])
+
+
 @pytest.mark.parametrize("dim", [8, 64])
 def test_int4_small_dim(gpu, oracle, dim):
     docs, offsets = ragged_fixture(40, 13, lo=1, hi=20, dim=dim)
