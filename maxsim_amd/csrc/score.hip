@@ -385,7 +385,10 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
           float y[L];
 #pragma unroll
           for (int l = 0; l < L; ++l)
-            y[l] = DOC == kDocSign ? (float)(2 * A.s[l][j][rr] - qsum[l][j]) : (float)A.s[l][j][rr];
+            // Sign documents: 2 (q . bits) - sum(q) as one fma on the
+            // converted dot (every term an integer below 2^24: exact).
+            y[l] = DOC == kDocSign ? fmaf((float)A.s[l][j][rr], 2.0f, (float)-qsum[l][j])
+                                   : (float)A.s[l][j][rr];
           Y = y[0];
           if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
         }
