@@ -20,14 +20,13 @@ struct ScoreWorkspace {
   DeviceBuffer cand_ids, cand_info, cand_tiles;
   // cascade: coarse scores, top-M candidates (scores / ids), fine scores
   DeviceBuffer coarse, top_m_scores, top_m_ids, fine;
-  DeviceBuffer cand_ranges;  // [batch][M][2] token ranges of the candidates (one per rescoring wave)
   // Synchronous calls: the fp32 query and the top-k results, in pinned host
   // memory that the kernels read and write directly.
   HostBuffer host_query, host_out;
   uint64_t bytes() const {
     return qpack.cap + qpack_alt.cap + colmul.cap + qsum.cap + weights.cap + pooled.cap + qbits.cap + full_info.cap +
            full_tiles.cap + cand_ids.cap + cand_info.cap + cand_tiles.cap + coarse.cap + top_m_scores.cap +
-           top_m_ids.cap + fine.cap + cand_ranges.cap;
+           top_m_ids.cap + fine.cap;
   }
 };
 
@@ -69,7 +68,6 @@ struct Targets {
   const int64_t* d_offsets = nullptr;
   int64_t max_doc_tiles = 1;
   bool tables_ready = false;  // the candidate tables are already in the workspace (select_topm wrote them)
-  const int64_t* d_ranges = nullptr;  // or the candidates' token ranges [batch][count][2] (one per wave)
 };
 
 // Wave layout of a per-row candidate rescoring pass (device targets): what

@@ -128,7 +128,6 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
       // document's token range (no tables).
       if (t.d_offsets == nullptr) throw InvalidArgument("device candidate lists need the token offsets");
       a.direct_offsets = t.d_offsets;
-      a.direct_ranges = t.d_ranges;
       a.direct_count = per_target;
       a.num_waves = w4;
     } else {
@@ -761,12 +760,10 @@ void check_cascade(int64_t k, int64_t m, int64_t num_docs) {
 // (score desc, document asc), put in document order -> fine scores of the
 // candidates -> top-k, ties by document id (cascade.py:294-453), all on the
 // device.  coarse(d_scores) and fine(d_candidate_ids, d_scores,
-// tables_ready, d_ranges) enqueue the two scoring passes.  With one
-// candidate per rescoring wave (`layout`, the rescoring pass's
-// candidate_layout) the pass needs no tables: the selector writes each
-// candidate's token range (d_ranges), so a wave reads its range with its
-// candidate instead of after it; with more, the selector writes the tables
-// itself, one launch fewer (tables_ready is then true).
+// tables_ready) enqueue the two scoring passes.  With one candidate per
+// rescoring wave (`layout`, the rescoring pass's candidate_layout) the pass
+// needs no tables; with more, the selector writes them itself, one launch
+// fewer (tables_ready is then true).
 template <typename Coarse, typename Fine>
 void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t k, int64_t m, Coarse coarse,
                     Fine fine, float* d_top_s, int64_t* d_top_i, hipStream_t stream, const CandidateLayout& layout,
@@ -775,18 +772,15 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
   coarse(ws.coarse.as<float>());
   ws.top_m_ids.ensure(sizeof(int64_t) * batch * m, "hipMalloc cascade candidates");
   bool tables_ready = false;
-  const int64_t* d_ranges = nullptr;
   if (num_docs <= kSortMaxRow) {
+    // One candidate per rescoring wave needs no tables (the pass reads each
+    // candidate's token range itself).
     const bool tables = layout.per_wave > 1;
     CandidateTables tab;
-    tab.d_offsets = d_offsets;
-    if (!tables) {
-      ws.cand_ranges.ensure(sizeof(int64_t) * 2 * batch * m, "hipMalloc cascade candidate token ranges");
-      tab.d_ranges = ws.cand_ranges.as<int64_t>();
-      d_ranges = tab.d_ranges;
-    } else {
+    if (tables) {
       ws.cand_info.ensure(sizeof(int64_t) * batch * layout.waves * kScoreInfoWords, "hipMalloc candidate wave table");
       ws.cand_tiles.ensure(sizeof(uint64_t) * batch * layout.waves * layout.cap, "hipMalloc candidate tile table");
+      tab.d_offsets = d_offsets;
       tab.waves = layout.waves;
       tab.per_wave = layout.per_wave;
       tab.cap = layout.cap;
@@ -794,7 +788,7 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
       tab.d_tiles = ws.cand_tiles.as<uint64_t>();
     }
     check_hip(launch_select_topm(ws.coarse.as<float>(), batch, num_docs, num_docs, m, ws.top_m_ids.as<int64_t>(),
-                                 stream, &tab),
+                                 stream, tables ? &tab : nullptr),
               "launch cascade candidate selection");
     tables_ready = tables;
   } else {
@@ -805,7 +799,7 @@ void cascade_device(ScoreWorkspace& ws, int64_t batch, int64_t num_docs, int64_t
     check_hip(launch_sort_rows(ws.top_m_ids.as<int64_t>(), batch, m, stream), "launch candidate sort");
   }
   ws.fine.ensure(sizeof(float) * batch * m, "hipMalloc cascade fine scores");
-  fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>(), tables_ready, d_ranges);
+  fine(ws.top_m_ids.as<int64_t>(), ws.fine.as<float>(), tables_ready);
   check_hip(launch_topk(ws.fine.as<float>(), batch, m, m, k, ws.top_m_ids.as<int64_t>(), d_top_s, d_top_i, stream),
             "launch cascade final selection");
 }
@@ -851,7 +845,7 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, qi, red, (float)temperature, batch,
                               query_tokens, wp, Targets{}, d, h->num_docs, nullptr, nullptr);
           },
-          [&](const int64_t* ids, float* d, bool tables_ready, const int64_t* ranges) {
+          [&](const int64_t* ids, float* d, bool tables_ready) {
             Targets t;
             t.device = ids;
             t.count = candidates;
@@ -859,7 +853,6 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
             t.d_offsets = h->offsets.as<int64_t>();
             t.max_doc_tiles = h->max_doc_tiles;
             t.tables_ready = tables_ready;
-            t.d_ranges = ranges;
             QueryInput again = qi;
             again.quantized = true;
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, again, red, (float)temperature, batch,
@@ -993,7 +986,7 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
         run_generic_score(h->ws, h->host_offsets, h->num_tokens, prefix, coarse_q, kRedMax, 1.0f, batch, query_tokens,
                           nullptr, Targets{}, d, h->num_docs, nullptr, stream);
       },
-      [&](const int64_t* ids, float* d, bool tables_ready, const int64_t* ranges) {
+      [&](const int64_t* ids, float* d, bool tables_ready) {
         Targets t;
         t.device = ids;
         t.count = m;
@@ -1001,7 +994,6 @@ void binres_cascade(msim_binary_docs* h, const float* d_query, int64_t batch, in
         t.d_offsets = h->offsets.as<int64_t>();
         t.max_doc_tiles = h->max_doc_tiles;
         t.tables_ready = tables_ready;
-        t.d_ranges = ranges;
         run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, fine_q, kRedMax, 1.0f, batch, query_tokens,
                           nullptr, t, d, m, nullptr, stream);
       },

@@ -139,14 +139,14 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
   __shared__ int64_t s_beg[kSortMaxRow];
   __shared__ uint32_t s_len[kSortMaxRow];
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const bool tables = tab.d_info != nullptr, ranges = tab.d_ranges != nullptr, spans = tables || ranges;
+  const bool tables = tab.d_info != nullptr;
   const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(scores + (int64_t)blockIdx.x * stride, (uint32_t)(n * 4));
-  const __amdgpu_buffer_rsrc_t roff = make_rsrc(spans ? tab.d_offsets : nullptr, spans ? (uint32_t)((n + 1) * 8) : 0u);
+  const __amdgpu_buffer_rsrc_t roff = make_rsrc(tables ? tab.d_offsets : nullptr, tables ? (uint32_t)((n + 1) * 8) : 0u);
   uint32_t v[E];
   int64_t beg[E], end[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = load_b32(rsrc, (e * kThreads + tid) * 4);
-  if (spans) {
+  if (tables) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       beg[e] = (int64_t)load_b64(roff, (e * kThreads + tid) * 8);
@@ -251,11 +251,6 @@ __global__ __launch_bounds__(1024) void select_topm_kernel(const float* __restri
         s_beg[r] = beg[e];
         s_len[r] = (uint32_t)(end[e] - beg[e]);
       }
-      if (ranges) {
-        int64_t* rg = tab.d_ranges + 2 * ((int64_t)blockIdx.x * m + r);
-        rg[0] = beg[e];
-        rg[1] = end[e];
-      }
     }
   if (!tables) return;
   // The rescoring pass's tables of this row (group), from the token ranges in
@@ -290,7 +285,6 @@ hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, i
   if (tab.d_info && (tab.d_tiles == nullptr || tab.d_offsets == nullptr || tab.waves <= 0 || tab.per_wave <= 0 ||
                      tab.waves * tab.per_wave < m))
     return hipErrorInvalidValue;
-  if (tab.d_ranges && tab.d_offsets == nullptr) return hipErrorInvalidValue;
   select_topm_kernel<<<dim3((unsigned)batch), dim3(1024), 0, stream>>>(d_scores, n, stride, m, d_out, tab);
   return hipGetLastError();
 }

@@ -183,9 +183,6 @@ struct ScoreArgs {
   // [direct_offsets[doc], direct_offsets[doc + 1]).
   const int64_t* direct_offsets;
   int64_t direct_count;
-  // Direct mode with the token ranges given: [groups][targets][2] (start,
-  // end) per target, read instead of direct_offsets (nullptr: unused).
-  const int64_t* direct_ranges;
   int64_t num_waves;           // per group, a multiple of 4
   int64_t info_grp_stride;     // int64 words between groups' wave tables (0 = shared)
   const int64_t* targets;      // document of each target, or nullptr (target = document)
@@ -246,9 +243,6 @@ struct CandidateTables {
   int64_t waves = 0, per_wave = 0, cap = 0;
   int64_t* d_info = nullptr;
   uint64_t* d_tiles = nullptr;
-  // Or (one candidate per rescoring wave): the selected documents' token
-  // ranges, [batch][m][2] (start, end) in position order.
-  int64_t* d_ranges = nullptr;
 };
 hipError_t launch_select_topm(const float* d_scores, int64_t batch, int64_t n, int64_t stride, int64_t m,
                               int64_t* d_out, hipStream_t stream, const CandidateTables* tables = nullptr);

@@ -208,15 +208,9 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   if (direct) {
     if (gw >= p.direct_count) return;  // no barriers below: a wave may leave early
     t0 = gw;
-    if (p.direct_ranges) {
-      const auto rg = as_constant(p.direct_ranges) + 2 * (grp * p.targets_grp_stride + gw);
-      ds = rg[0];
-      de = rg[1];
-    } else {
-      const int64_t doc = targets[gw];
-      ds = as_constant(p.direct_offsets)[doc];
-      de = as_constant(p.direct_offsets)[doc + 1];
-    }
+    const int64_t doc = targets[gw];
+    ds = as_constant(p.direct_offsets)[doc];
+    de = as_constant(p.direct_offsets)[doc + 1];
     ntiles = ds == de ? 1 : (int)((de - ds + 15) / 16);
   } else {
     const auto info = as_constant(p.wave_info) + grp * p.info_grp_stride + gw * kScoreInfoWords;
