@@ -254,6 +254,25 @@ def test_binary_fp32_maxsim_matches_reference_lut(gpu, oracle, shape):
     _close(got, exp)
 
 
+def test_binary_fp32_topk_consecutive_calls(gpu, oracle):
+    """The binary handle's synchronous top-k also stages its query and results
+    in pinned host memory: calls in a row with other queries, shapes and k
+    each match the reference LUT scores of their own query."""
+    docs, offsets = ragged_fixture(150, 26, lo=1, hi=40)
+    codes, h = _binary_handle(oracle, docs, offsets)
+    rng = np.random.default_rng(27)
+    queries = [rng.standard_normal(s + (128,)).astype(np.float32) for s in [(2, 5), (3, 32), (1, 2)]]
+    for i, (query, k) in enumerate([(queries[0], 7), (queries[1], 20), (queries[0], 7), (queries[2], 3)]):
+        print(f"call {i}: query {query.shape} k={k}", flush=True)
+        scores = h.maxsim_batch(query)
+        _close(scores, np.stack([oracle.binary_lut_maxsim(qb, codes, offsets, 128, 1.0) for qb in query]))
+        top_s, top_i = h.topk_batch(query, k)
+        for row, si, ii in zip(scores, top_s, top_i):
+            order = np.lexsort((np.arange(row.shape[0]), -row))[:k]
+            np.testing.assert_array_equal(ii, order)
+            np.testing.assert_array_equal(si, row[order])
+
+
 @pytest.mark.parametrize("reducer", REDUCERS)
 def test_binary_reducers_with_scales(gpu, oracle, reducer):
     docs, offsets, query, weights, cand = _reducer_fixture()
