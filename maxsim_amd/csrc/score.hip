@@ -52,7 +52,8 @@ template <>
 struct ReducerState<kRedMax> {
   float m;
   __device__ void init() { m = kNegInf; }
-  __device__ void add4(const float (&z)[4], float) { m = fmaxf(fmaxf(m, fmaxf(z[0], z[1])), fmaxf(z[2], z[3])); }
+  // Two three-way maxima (v_max3_f32) for four values: exact, any order.
+  __device__ void add4(const float (&z)[4], float) { m = max3_op(max3_op(m, z[0], z[1]), z[2], z[3]); }
   __device__ void merge_xor(int mask, float) { m = fmaxf(m, __shfl_xor(m, mask)); }
   __device__ float finish(int len, float colmul, float, float weight, float doc_scale) const {
     return len == 0 ? 0.0f : m * colmul * weight * doc_scale;
