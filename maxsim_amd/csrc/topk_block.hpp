@@ -533,7 +533,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   auto expired = [&]() { return __builtin_amdgcn_s_memrealtime() - t_start > kTailWaitTicks; };
   auto give_up = [&]() {
     if (lane < k) {
-      out_s[lane] = __builtin_nanf("");
+      out_s[lane] = __uint_as_float(0x7FC00000u);  // quiet NaN by its bits (device code is built without NaN semantics)
       out_i[lane] = -1;
     }
   };
