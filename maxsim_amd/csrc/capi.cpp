@@ -423,14 +423,6 @@ float* ensure_scores(msim_int4_docs* h, int64_t batch, int64_t targets) {
   return h->scores.as<float>();
 }
 
-float* upload_query(msim_int4_docs* h, const float* query, int64_t batch, int64_t query_tokens,
-                    int64_t dim, hipStream_t stream) {
-  const size_t bytes = sizeof(float) * (size_t)(batch * query_tokens * dim);
-  h->query.ensure(std::max<size_t>(bytes, 4), "hipMalloc query cache");
-  if (bytes) check_hip(hipMemcpyAsync(h->query.ptr, query, bytes, hipMemcpyHostToDevice, stream), "copy query to device");
-  return h->query.as<float>();
-}
-
 }  // namespace
 
 extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64_t row_bytes,
@@ -559,11 +551,20 @@ extern "C" int msim_int4_maxsim_batch_int8q(msim_int4_docs* h, const float* quer
     if (batch == 0 || h->num_docs == 0) return;
     select_device(h->device);
     hipStream_t stream = nullptr;
-    float* d_query = upload_query(h, query, batch, query_tokens, dim, stream);
+    // The query and the score rows pass through the handle's pinned buffer:
+    // the quantisation kernel reads the query there, and the scores come
+    // back by one DMA copy into it.
+    const size_t qbytes = sizeof(float) * (size_t)(batch * query_tokens * dim);
+    const size_t obytes = sizeof(float) * (size_t)(batch * h->num_docs);
+    const size_t q_al = (qbytes + 255) & ~(size_t)255;
+    h->host_io.ensure(q_al + obytes, "hipHostMalloc int8q query and score staging");
+    char* io = h->host_io.as<char>();
+    std::memcpy(io, query, qbytes);
     float* d_scores = ensure_scores(h, batch, h->num_docs);
-    run_int8q(h, d_query, batch, query_tokens, d_scores, stream);
-    check_hip(hipMemcpyAsync(out, d_scores, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost, stream), "copy int8q output to host");
+    run_int8q(h, reinterpret_cast<const float*>(io), batch, query_tokens, d_scores, stream);
+    check_hip(hipMemcpyAsync(io + q_al, d_scores, obytes, hipMemcpyDeviceToHost, stream), "copy int8q output to host");
     check_hip(hipStreamSynchronize(stream), "synchronize int4 int8q maxsim");
+    std::memcpy(out, io + q_al, obytes);
   });
 }
 

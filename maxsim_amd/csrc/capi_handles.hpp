@@ -114,8 +114,8 @@ struct msim_int4_docs {
   // per-token 1/16 when the corpus has no token scales.
   msim::DeviceBuffer codes128, residual128, ones16;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
-  msim::DeviceBuffer query, qpack, qscale, qbias, scores, rowmax;
-  msim::HostBuffer host_io;  // synchronous top-k: query in, results out (pinned)
+  msim::DeviceBuffer qpack, qscale, qbias, scores, rowmax;
+  msim::HostBuffer host_io;  // synchronous calls: query in, results out (pinned)
   // Scan with fused top-k: launch counter, key rows of kScanTailRow tagged
   // 64-bit keys and workgroup records (3 x kScanTailBlocks tagged words per row).
   msim::DeviceBuffer tail_epoch, tail_keys, tail_rec;
@@ -126,7 +126,7 @@ struct msim_int4_docs {
            residual_token_scales16.cap + codes128.cap + residual128.cap + ones16.cap;
   }
   uint64_t workspace_bytes() const {
-    return query.cap + qpack.cap + qscale.cap + qbias.cap + scores.cap +
+    return qpack.cap + qscale.cap + qbias.cap + scores.cap +
            rowmax.cap + wave_info.cap + tile_table.cap + tail_epoch.cap + tail_keys.cap + tail_rec.cap + ws.bytes();
   }
 };

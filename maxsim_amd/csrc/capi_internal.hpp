@@ -85,10 +85,10 @@ struct DeviceBuffer {
   }
 };
 
-// Pinned, coherent host memory that only grows.  The synchronous top-k entry
+// Pinned, coherent host memory that only grows.  The synchronous entry
 // points stage the query and the results there: the kernels read the query
-// and write the results across the host link themselves, so a call makes no
-// staging copies of its own.
+// and write top-k results across the host link themselves (a full score
+// matrix comes back by one DMA copy), so no pageable staging copies remain.
 struct HostBuffer {
   void* ptr = nullptr;
   size_t cap = 0;
