@@ -326,6 +326,15 @@ struct HostTopk {
   }
 };
 
+// A full score matrix of a synchronous call: one DMA copy into the
+// workspace's pinned host buffer, then out of it once the stream is done.
+void copy_scores_out(ScoreWorkspace& ws, void* out, const void* d, size_t bytes) {
+  ws.host_out.ensure(std::max<size_t>(bytes, 8), "hipHostMalloc score staging");
+  check_hip(hipMemcpyAsync(ws.host_out.ptr, d, bytes, hipMemcpyDeviceToHost, nullptr), "copy output to host");
+  check_hip(hipStreamSynchronize(nullptr), "synchronize score copy");
+  std::memcpy(out, ws.host_out.ptr, bytes);
+}
+
 // ------------------------------------------------------------------ int4
 
 DocStreams int4_streams(msim_int4_docs* h, bool residual) {
@@ -385,7 +394,7 @@ extern "C" int msim_int4_maxsim_batch(msim_int4_docs* h, const float* query, int
     if (batch == 0 || h->num_docs == 0) return;
     select_device(h->device);
     float* d = int4_score_device(h, query, batch, query_tokens, dim, kRedMax, {}, 1.0f, nullptr, 0, false, nullptr);
-    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+    copy_scores_out(h->ws, out, d, sizeof(float) * batch * h->num_docs);
   });
 }
 
@@ -426,7 +435,7 @@ extern "C" int msim_int4_score(msim_int4_docs* h, const float* query, int64_t ba
     select_device(h->device);
     float* d = int4_score_device(h, query, batch, query_tokens, dim, red, w, (float)temperature, candidates,
                                  num_candidates, residual != 0, nullptr);
-    check_hip(hipMemcpy(out, d, sizeof(float) * batch * targets, hipMemcpyDeviceToHost), "copy output to host");
+    copy_scores_out(h->ws, out, d, sizeof(float) * batch * targets);
   });
 }
 
@@ -594,7 +603,7 @@ extern "C" int msim_binary_maxsim_batch(msim_binary_docs* h, const float* query,
     select_device(h->device);
     const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
     float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, kRedMax, {}, 1.0f, nullptr, 0);
-    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+    copy_scores_out(h->ws, out, d, sizeof(float) * batch * h->num_docs);
   });
 }
 
@@ -624,7 +633,7 @@ extern "C" int msim_binary_maxsim_batch_int8q(msim_binary_docs* h, const float* 
     select_device(h->device);
     const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, nullptr);
     float* d = binary_score_device(h, query, batch, query_tokens, dim, 1, true, s, kRedMax, {}, 1.0f, nullptr, 0);
-    check_hip(hipMemcpy(out, d, sizeof(float) * batch * h->num_docs, hipMemcpyDeviceToHost), "copy output to host");
+    copy_scores_out(h->ws, out, d, sizeof(float) * batch * h->num_docs);
   });
 }
 
@@ -669,7 +678,7 @@ extern "C" int msim_binary_score(msim_binary_docs* h, const float* query, int64_
     const DocStreams s = binary_streams(h, scale, use_scale_vector, use_token_scale, d_override);
     float* d = binary_score_device(h, query, batch, query_tokens, dim, 3, false, s, red, w, (float)temperature,
                                    candidates, num_candidates);
-    check_hip(hipMemcpy(out, d, sizeof(float) * batch * targets, hipMemcpyDeviceToHost), "copy output to host");
+    copy_scores_out(h->ws, out, d, sizeof(float) * batch * targets);
   });
 }
 
@@ -707,8 +716,7 @@ extern "C" int msim_binary_hamming_batch(msim_binary_docs* h, const uint8_t* qbi
     const uint8_t* d_q = upload_qbits(h, qbits, batch * query_tokens);
     h->iscores.ensure(sizeof(int32_t) * batch * h->num_docs, "hipMalloc hamming scores");
     hamming_device(h, d_q, batch, query_tokens, nullptr, h->iscores.as<int32_t>(), nullptr);
-    check_hip(hipMemcpy(out, h->iscores.ptr, sizeof(int32_t) * batch * h->num_docs, hipMemcpyDeviceToHost),
-              "copy hamming scores to host");
+    copy_scores_out(h->ws, out, h->iscores.ptr, sizeof(int32_t) * batch * h->num_docs);
   });
 }
 
@@ -1072,8 +1080,7 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
     if (!scanned)
       run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr, t,
                         h->scores.as<float>(), targets, nullptr, nullptr);
-    check_hip(hipMemcpy(out, h->scores.ptr, sizeof(float) * batch * targets, hipMemcpyDeviceToHost),
-              "copy output to host");
+    copy_scores_out(h->ws, out, h->scores.ptr, sizeof(float) * batch * targets);
   });
 }
 
