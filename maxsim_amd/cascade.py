@@ -160,6 +160,26 @@ def residual_score(query_tokens, packed: ResidualInt4PackedDocs, *, device: str 
     return result[0] if squeeze else result
 
 
+def _residual_topk(query_tokens, packed: ResidualInt4PackedDocs, k: int, *, device: str = "auto",
+                   reducer: str = "maxsim", query_weights=None, temperature: float = 1.0):
+    """Top-k of the fused scores over every document, selected on the device:
+    the same result as ``_stable_topk(residual_score(...), k)`` (score desc,
+    document id asc; the sdk's full residual search, sdk.py:497-559) without
+    bringing the [B, N] scores to the host."""
+    _validate_residual_packed(packed)
+    batches, squeeze = _normalize_query(query_tokens, packed.dim)
+    reducer_value, weights, temperature_value = _normalize_reducer_options(
+        reducer, query_weights, temperature, batch=batches.shape[0], query_tokens=batches.shape[1])
+    if batches.shape[0] == 0 or batches.shape[1] == 0:
+        return _stable_topk(residual_score(query_tokens, packed, device=device, reducer=reducer,
+                                           query_weights=query_weights, temperature=temperature), k)
+    resident = _on_device(packed, device)
+    scores, indices = resident.prefix_data.topk_score_batch(np.ascontiguousarray(batches, dtype=np.float32), int(k),
+                                                            reducer_value, weights, float(temperature_value),
+                                                            residual=True)
+    return (scores[0], indices[0]) if squeeze else (scores, indices)
+
+
 def cascade_topk(query_tokens, packed: ResidualInt4PackedDocs, k: int, *, candidates: int, device: str = "auto",
                  reducer: str = "maxsim", query_weights=None, temperature: float = 1.0):
     """Prefix top-``candidates`` -> fused rescoring -> top-k (cascade.py:294-393).

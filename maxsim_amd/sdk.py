@@ -27,7 +27,14 @@ from maxsim_amd.binres import (
     binres_to_device,
     pack_binary_residual,
 )
-from maxsim_amd.cascade import _stable_topk, cascade_topk, pack_residual_int4, residual_int4_to_device, residual_score
+from maxsim_amd.cascade import (
+    _residual_topk,
+    _stable_topk,
+    cascade_topk,
+    pack_residual_int4,
+    residual_int4_to_device,
+    residual_score,
+)
 from maxsim_amd.experimental import int4_maxsim, int4_to_device, pack_int4_symmetric, topk_int4_maxsim
 
 MODES = (
@@ -211,8 +218,7 @@ class Reranker:
             scores, indices = topk_maxsim(query_embeddings, self.corpus.packed, kk, device="auto", **opts)
         elif mode == "int4_residual":
             if rescore_candidates is None:
-                scores, indices = _stable_topk(residual_score(query_embeddings, self.corpus.int4_packed,
-                                                              device="auto", **opts), kk)
+                scores, indices = _residual_topk(query_embeddings, self.corpus.int4_packed, kk, device="auto", **opts)
             else:
                 scores, indices = cascade_topk(query_embeddings, self.corpus.int4_packed, kk,
                                                candidates=rescore_candidates, device="auto", **opts)

@@ -62,6 +62,33 @@ def test_residual_mode_search_rerank_cascade(gpu):
     assert [x.doc_id for x in reranked] == [["doc-4", "doc-1", "doc-3"][i] for i in order]
 
 
+@pytest.mark.parametrize("reducer", ["maxsim", "weighted_maxsim", "topk2", "topk4", "smoothsim"])
+def test_residual_full_search_equals_stable_topk_of_the_scores(gpu, reducer):
+    """Reranker.search on an int4_residual index without rescore_candidates
+    selects on the device; it must return what the reference's search does
+    (its stable top-k of the fused scores, sdk.py:497-559), ties included
+    (every document appears twice)."""
+    from maxsim_amd.cascade import _stable_topk, residual_score
+
+    rng = np.random.default_rng(211)
+    lengths = rng.integers(1, 12, size=60)
+    lengths = np.concatenate([lengths, lengths])
+    offsets = np.concatenate(([0], np.cumsum(lengths))).astype(np.int64)
+    half = rng.normal(size=(int(lengths[:60].sum()), 128)).astype(np.float32)
+    docs = np.concatenate([half, half])
+    ids = [f"d{i}" for i in range(120)]
+    corpus = maxsim.Index.from_embeddings(ids, docs, offsets, mode="int4_residual")
+    r = maxsim.Reranker.from_corpus(corpus, device="cuda")
+    query = rng.normal(size=(3, 7, 128)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, size=(3, 7)).astype(np.float32) if reducer == "weighted_maxsim" else None
+    opts = dict(reducer=reducer, query_weights=w, temperature=0.7)
+    es, ei = _stable_topk(residual_score(query, corpus.int4_packed, **opts), 15)
+    res = r.search(query, k=15, **opts)
+    for row, s, i in zip(res, es, ei):
+        assert [x.doc_id for x in row] == [ids[j] for j in i]
+        assert [x.score for x in row] == [float(v) for v in s]
+
+
 def test_rescore_candidates_requires_residual_mode(gpu):
     with pytest.raises(ValueError, match="int4_residual"):
         _reranker("int4_per_token").search(np.ones((1, 8), np.float32), k=2, rescore_candidates=3)
