@@ -350,6 +350,14 @@ int msim_binary_get_rescore_limbs(const msim_binary_docs* h, int* limbs);
 int msim_binary_binres_score(msim_binary_docs* h, const float* query, int64_t batch,
                              int64_t query_tokens, int64_t dim, int fused, const int64_t* candidates,
                              int64_t num_candidates, float* out);
+/* No counterpart in the reference (its format has no binary prefix).  Top-k
+ * of the fused scores of every document (score desc, id asc), selected on
+ * the device: what a full search of this format returns, without the
+ * [B, N] scores leaving the device.  out_scores f32 [B, k], out_indices
+ * i64 [B, k]; 1 <= k <= num_docs. */
+int msim_binary_binres_topk(msim_binary_docs* h, const float* query, int64_t batch,
+                            int64_t query_tokens, int64_t dim, int64_t k, float* out_scores,
+                            int64_t* out_indices);
 /* Coarse top-M -> fused rescoring -> top-k, on the device (the cascade of
  * msim_int4_cascade_topk over this format). */
 int msim_binary_cascade_topk(msim_binary_docs* h, const float* query, int64_t batch,

@@ -523,6 +523,17 @@ class CudaPackedDocs:
                                                  0 if cand is None else cand.shape[1], ptr(out)))
         return out
 
+    def binres_topk_batch(self, query, k):
+        """Top-k of the fused scores of every document, selected on the device."""
+        q = _query3(query)
+        k = int(k)
+        if k < 1 or k > self.num_docs:
+            raise ValueError("k must be between 1 and num_docs")
+        scores = np.empty((q.shape[0], k), np.float32)
+        indices = np.empty((q.shape[0], k), np.int64)
+        check(self._lib.msim_binary_binres_topk(self._h, ptr(q), *q.shape, k, ptr(scores), ptr(indices)))
+        return scores, indices
+
     def cascade_topk(self, query, k, candidates):
         q = _query3(query)
         k, m = int(k), int(candidates)

@@ -85,6 +85,7 @@ SIGNATURES: dict[str, list] = {
     "msim_binary_set_rescore_limbs": [c_vp, c_int],
     "msim_binary_get_rescore_limbs": [c_vp, c_vp],
     "msim_binary_binres_score": [c_vp, c_vp, c_i64, c_i64, c_i64, c_int, c_vp, c_i64, c_vp],
+    "msim_binary_binres_topk": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_binary_cascade_topk": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp],
     "msim_binary_cascade_topk_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
 }

@@ -27,6 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from maxsim_amd._api import _as_numpy, _normalize_offsets
+from maxsim_amd.cascade import _stable_topk
 from maxsim_amd.experimental import pack_int4_symmetric
 
 
@@ -134,6 +135,19 @@ def binres_score(query_tokens, packed: BinaryResidualPackedDocs, *, fused: bool 
     with _RescorePrecision(resident.sign_data, query_precision):
         out = resident.sign_data.binres_score_batch(q, fused=fused, candidate_indices=cand)
     return out[0] if squeeze else out
+
+
+def _binres_topk(query_tokens, packed: BinaryResidualPackedDocs, k: int, *, query_precision: str = "int8"):
+    """Top-k of the fused scores of every document (score desc, id asc),
+    selected on the device: the same result as the stable top-k of
+    ``binres_score(...)`` without the [B, N] scores leaving the device."""
+    q, squeeze = _query(query_tokens, packed.dim)
+    if q.shape[0] == 0 or q.shape[1] == 0:
+        return _stable_topk(binres_score(query_tokens, packed, query_precision=query_precision), k)
+    resident = binres_to_device(packed)
+    with _RescorePrecision(resident.sign_data, query_precision):
+        scores, indices = resident.sign_data.binres_topk_batch(q, int(k))
+    return (scores[0], indices[0]) if squeeze else (scores, indices)
 
 
 def binres_cascade_topk(query_tokens, packed: BinaryResidualPackedDocs, k: int, *, candidates: int,

@@ -1084,6 +1084,28 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
   });
 }
 
+extern "C" int msim_binary_binres_topk(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
+                                       int64_t dim, int64_t k, float* out_scores, int64_t* out_indices) {
+  return guarded([&] {
+    require_handle(h);
+    check_binary_query(h, batch, query_tokens, dim);
+    check_k(k, h->num_docs);
+    const DocStreams s = binres_streams(h, true);
+    if (batch == 0) return;
+    select_device(h->device);
+    QueryInput qi;
+    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    qi.limbs = h->rescore_limbs;
+    h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
+    run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr,
+                      Targets{}, h->scores.as<float>(), h->num_docs, nullptr, nullptr);
+    const HostTopk out(h->ws, batch, k);
+    check_hip(launch_topk(h->scores.as<float>(), batch, h->num_docs, h->num_docs, k, nullptr, out.s, out.i, nullptr),
+              "launch topk selection kernel");
+    out.finish(out_scores, out_indices, nullptr);
+  });
+}
+
 extern "C" int msim_binary_cascade_topk(msim_binary_docs* h, const float* query, int64_t batch, int64_t query_tokens,
                                         int64_t dim, int64_t k, int64_t candidates, float* out_scores,
                                         int64_t* out_indices) {

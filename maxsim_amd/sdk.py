@@ -22,6 +22,7 @@ import numpy as np
 from maxsim_amd._api import PackedDocs, _as_numpy, maxsim, pack_signs, to_device, topk_maxsim
 from maxsim_amd.binres import (
     BinaryResidualPackedDocs,
+    _binres_topk,
     binres_cascade_topk,
     binres_score,
     binres_to_device,
@@ -29,7 +30,6 @@ from maxsim_amd.binres import (
 )
 from maxsim_amd.cascade import (
     _residual_topk,
-    _stable_topk,
     cascade_topk,
     pack_residual_int4,
     residual_int4_to_device,
@@ -225,7 +225,7 @@ class Reranker:
         elif mode == "binary_residual":
             _require_maxsim_reducer(mode, reducer, query_weights, temperature)
             if rescore_candidates is None:
-                scores, indices = _stable_topk(binres_score(query_embeddings, self.corpus.int4_packed), kk)
+                scores, indices = _binres_topk(query_embeddings, self.corpus.int4_packed, kk)
             else:
                 scores, indices = binres_cascade_topk(query_embeddings, self.corpus.int4_packed, kk,
                                                       candidates=rescore_candidates)

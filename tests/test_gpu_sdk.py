@@ -131,6 +131,32 @@ def test_binary_residual_mode(gpu, oracle):
         np.testing.assert_allclose(got, exp[b][idx], rtol=1e-6, atol=1e-5)
 
 
+@pytest.mark.parametrize("precision", ["int8", "fp32"])
+def test_binary_residual_full_search_equals_stable_topk_of_the_scores(gpu, precision):
+    """The full search of a binary_residual index selects on the device; it
+    returns the stable top-k of the fused scores (score desc, id asc), ties
+    included (every document appears twice), for both query precisions."""
+    from maxsim_amd.binres import _binres_topk, binres_score, pack_binary_residual
+    from maxsim_amd.cascade import _stable_topk
+
+    rng = np.random.default_rng(223)
+    lengths = rng.integers(1, 20, size=80)
+    lengths = np.concatenate([lengths, lengths])
+    offsets = np.concatenate(([0], np.cumsum(lengths))).astype(np.int64)
+    half = rng.normal(size=(int(lengths[:80].sum()), 128)).astype(np.float32)
+    packed = pack_binary_residual(np.concatenate([half, half]), offsets)
+    query = rng.normal(size=(3, 9, 128)).astype(np.float32)
+    es, ei = _stable_topk(binres_score(query, packed, query_precision=precision), 12)
+    gs, gi = _binres_topk(query, packed, 12, query_precision=precision)
+    np.testing.assert_array_equal(gi, ei)
+    np.testing.assert_array_equal(gs, es)
+    ids = [f"d{i}" for i in range(160)]
+    index = maxsim.Index.from_embeddings(ids, np.concatenate([half, half]), offsets, mode="binary_residual")
+    res = maxsim.Reranker(index, device="cuda").search(query, k=12)
+    if precision == "int8":
+        assert [[x.doc_id for x in row] for row in res] == [[ids[j] for j in row] for row in ei]
+
+
 @pytest.mark.parametrize("mode", ["binary_token_scale", "int4_per_token", "int4_residual", "binary_residual"])
 def test_saved_index_searches_the_same(gpu, tmp_path, mode):
     """tests/test_sdk.py:130-306: an index read back from its .npz file gives
