@@ -55,6 +55,15 @@ int msim_get_docs_per_wave(void);
  * (cuda_extension.cu:1629-1692 returns full score rows). */
 int msim_set_fused_topk(int mode);
 int msim_get_fused_topk(void);
+/* How long the fused selection waits for the other workgroups' results, in
+ * ticks of the GPU's 100 MHz real-time counter (default 10,000,000 = 100 ms;
+ * the wait normally ends within microseconds).  A selection whose wait runs
+ * out gives up: it writes id -1 and a NaN score into every slot of its batch
+ * row and adds one to the handle's give-up counter (msim_int4_fused_giveups).
+ * 0 makes every fused selection give up before reading anything (for tests of
+ * that path).  No counterpart in the reference. */
+int msim_set_fused_wait_ticks(int64_t ticks);
+int64_t msim_get_fused_wait_ticks(void);
 /* Prefix (sign) pass of the binary-prefix + int4-residual cascade
  * (msim_binary_cascade_topk*): 1 (default) = the int8-query scan kernel
  * over the sign stream when it applies (query rows of <= 128 tokens, token
@@ -133,7 +142,9 @@ int msim_int4_get_props(const msim_int4_docs* h, msim_int4_props* out);
  * out: host [B, N]. */
 int msim_int4_maxsim_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
                                  int64_t query_tokens, int64_t dim, float* out);
-/* topk_batch_int8q(query, k) -> (f32[B,k], i64[B,k]) (cu:3008-3033). */
+/* topk_batch_int8q(query, k) -> (f32[B,k], i64[B,k]) (cu:3008-3033).
+ * Fails with MSIM_ERUNTIME if the fused selection gave up (see
+ * msim_set_fused_wait_ticks): it never returns id -1. */
 int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query, int64_t batch,
                                int64_t query_tokens, int64_t dim, int64_t k,
                                float* out_scores, int64_t* out_indices);
@@ -148,6 +159,14 @@ int msim_int4_maxsim_int8q_async(msim_int4_docs* h, const float* d_query, int64_
 int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t batch,
                                int64_t query_tokens, int64_t k, float* d_scores,
                                int64_t* d_indices, void* stream);
+/* Sentinel of the *_async and _noalloc top-k calls of the int8-query path:
+ * a batch row whose fused selection gave up holds id -1 and a NaN score in
+ * every slot (see msim_set_fused_wait_ticks); callers that read results
+ * without a synchronous call check d_indices for -1.  The number of
+ * selections that gave up on this handle so far (noalloc calls are not
+ * counted here): waits for the device, then reads it.  No counterpart in the
+ * reference. */
+int msim_int4_fused_giveups(const msim_int4_docs* h, uint64_t* out);
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): msim_int4_topk_int8q_async with the same arguments and
@@ -162,7 +181,8 @@ int msim_int4_topk_int8q_async(msim_int4_docs* h, const float* d_query, int64_t 
  * msim_set_scan_partition changes, one msim_int4_topk_int8q_async call must
  * rebuild them first.  The first call on a device looks the array up
  * (make it outside graph capture).  All calls on one GPU share the array:
- * calls that overlap on one GPU race. */
+ * calls that overlap on one GPU race.  A row whose fused selection gave up
+ * holds the id -1 / NaN sentinel described above. */
 int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_query, int64_t batch,
                                  int64_t query_tokens, int64_t k, float* d_scores,
                                  int64_t* d_indices, void* stream);

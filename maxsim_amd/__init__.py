@@ -32,11 +32,12 @@ from maxsim_amd.experimental import (
     topk_int4_maxsim,
 )
 
-from maxsim_amd.sdk import MODE_PRESETS, Corpus, Index, Reranker, SearchResult
+from maxsim_amd.sdk import MODE_PRESETS, Corpus, CorpusMemoryReport, Index, Reranker, SearchResult
 
 __all__ = [
     "BinaryResidualPackedDocs",
     "Corpus",
+    "CorpusMemoryReport",
     "Index",
     "MODE_PRESETS",
     "Reranker",

@@ -14,6 +14,7 @@ Every scoring call runs on the GPU through HIP kernels; there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import threading as _threading
 
 import numpy as np
 
@@ -80,6 +81,114 @@ def set_fused_topk(mode: int) -> None:
 
 def get_fused_topk() -> int:
     return int(_native.load().msim_get_fused_topk())
+
+
+def set_fused_wait_ticks(ticks: int) -> None:
+    """How long the int8-query search's fused selection waits for the scan's
+    other workgroups, in ticks of the GPU's 100 MHz clock (default 10**7 =
+    100 ms).  A selection that runs out of time gives up: synchronous calls
+    raise RuntimeError, the *_async forms leave id -1 / NaN in the row.  0
+    makes every fused selection give up at once (tests of that path)."""
+    check(_native.load().msim_set_fused_wait_ticks(int(ticks)))
+
+
+def get_fused_wait_ticks() -> int:
+    return int(_native.load().msim_get_fused_wait_ticks())
+
+
+# The reference module's launch-shape knobs (cuda_extension.cu:24-76,
+# 3482-3513).  They pick among the reference's SM89 kernels: shared-memory
+# reducer warps, residual reducer warps, and the dim-128 unrolled / q-tiled
+# binary kernels.  Every gfx950 scoring path here is one MFMA kernel whose
+# launch shape comes from the corpus (msim_set_docs_per_wave), so these
+# settings change no result and no launch.  They are kept with the
+# reference's defaults, scope (the warp knobs per thread, the dim-128 ones
+# per process), validation and messages, so that code and tests written
+# against the reference's module run unchanged.
+_routing = _threading.local()
+_dim128_unrolled_min_avg_tokens = 256
+_dim128_qtile_min_packed_bytes = (1 << 64) - 1
+
+
+def _thread_knob(name: str, default: int) -> int:
+    return int(getattr(_routing, name, default))
+
+
+def set_shared_reducer_warps(value: int) -> None:
+    """Reference: cu:3486-3492 (no effect on gfx950)."""
+    value = int(value)
+    if value not in (0, 4, 8):
+        raise ValueError("shared reducer warps must be one of 0, 4, or 8")
+    _routing.shared_reducer_warps = value
+
+
+def get_shared_reducer_warps() -> int:
+    return _thread_knob("shared_reducer_warps", 4)
+
+
+def set_residual_reducer_warps(value: int) -> None:
+    """Reference: cu:3493-3499 (no effect on gfx950)."""
+    value = int(value)
+    if value not in (0, 4, 8):
+        raise ValueError("residual reducer warps must be one of 0, 4, or 8")
+    _routing.residual_reducer_warps = value
+
+
+def get_residual_reducer_warps() -> int:
+    return _thread_knob("residual_reducer_warps", 8)
+
+
+def set_residual_reducer_force_warps(value: int) -> None:
+    """Reference: cu:3500-3507 (no effect on gfx950)."""
+    value = int(value)
+    if value not in (-1, 0, 4, 8):
+        raise ValueError("residual reducer force warps must be one of -1, 0, 4, or 8")
+    _routing.residual_reducer_force_warps = value
+
+
+def get_residual_reducer_force_warps() -> int:
+    return _thread_knob("residual_reducer_force_warps", -1)
+
+
+def get_effective_residual_reducer_warps(query_tokens: int) -> int:
+    """The reference's residual launch policy (cu:58-76) applied to the knobs
+    above; reported only."""
+    query_tokens = int(query_tokens)
+    if query_tokens <= 0:
+        raise ValueError("query tokens must be positive")
+    forced = get_residual_reducer_force_warps()
+    if forced >= 0:
+        return forced
+    warps = get_residual_reducer_warps()
+    if warps == 8:
+        return 8 if query_tokens >= 8 else 4
+    return warps if warps <= query_tokens else 0
+
+
+def set_dim128_unrolled_min_avg_tokens(value: int) -> None:
+    """Reference: cu:3482 (no effect on gfx950)."""
+    global _dim128_unrolled_min_avg_tokens
+    _dim128_unrolled_min_avg_tokens = int(value)
+
+
+def get_dim128_unrolled_min_avg_tokens() -> int:
+    return _dim128_unrolled_min_avg_tokens
+
+
+def set_dim128_qtile_min_packed_bytes(value: int) -> None:
+    """Reference: cu:3484 (no effect on gfx950).  The reference's argument is a
+    size_t: negative values and values of 2**64 or more are rejected."""
+    global _dim128_qtile_min_packed_bytes
+    if isinstance(value, bool) or not isinstance(value, (int, np.integer)):
+        raise TypeError("set_dim128_qtile_min_packed_bytes(): incompatible function arguments")
+    value = int(value)
+    if value < 0 or value >= (1 << 64):
+        raise TypeError("set_dim128_qtile_min_packed_bytes(): incompatible function arguments")
+    _dim128_qtile_min_packed_bytes = value
+
+
+def get_dim128_qtile_min_packed_bytes() -> int:
+    return _dim128_qtile_min_packed_bytes
 
 
 def set_prefix_scan(mode: int) -> None:
@@ -247,9 +356,17 @@ class CudaInt4PackedDocs:
         check(self._lib.msim_int4_maxsim_int8q_async(self._h, ptr(query), b, q, ptr(out),
                                                      _stream_ptr(stream)))
 
+    def fused_giveups(self) -> int:
+        """Fused int8-query selections of this handle that gave up waiting
+        (their rows hold id -1); waits for the device first."""
+        out = ctypes.c_uint64()
+        check(self._lib.msim_int4_fused_giveups(self._h, ctypes.byref(out)))
+        return int(out.value)
+
     def topk_int8q_async(self, query, k, scores, indices, stream=None):
         """Enqueue int8-query MaxSim + top-k on device tensors (scores f32[B,k],
-        indices i64[B,k])."""
+        indices i64[B,k]).  A row whose fused selection gave up holds id -1 and
+        NaN scores (see set_fused_wait_ticks)."""
         b, q = int(query.shape[0]), int(query.shape[1])
         check(self._lib.msim_int4_topk_int8q_async(self._h, ptr(query), b, q, int(k), ptr(scores),
                                                    ptr(indices), _stream_ptr(stream)))
@@ -596,7 +713,20 @@ class CudaPackedDocs:
 
     @property
     def maxsim_kernel_variant(self) -> str:
-        return "mfma_sign_i8"
+        """The reference's route label for this corpus (cu:2342-2347, 2625-2634:
+        "dim128_qtile" when dim is 128 and packed_size reaches
+        get_dim128_qtile_min_packed_bytes(), "dim128_unrolled" for dim 128 with
+        at most 128 documents or an average of at least
+        get_dim128_unrolled_min_avg_tokens() tokens, else "generic").  On
+        gfx950 all three routes are the same MFMA sign-document scorer."""
+        if self.dim != 128:
+            return "generic"
+        if self.packed_size >= _dim128_qtile_min_packed_bytes:
+            return "dim128_qtile"
+        if self.num_docs <= 128:
+            return "dim128_unrolled"
+        avg_tokens = self.num_tokens // max(self.num_docs, 1)
+        return "dim128_unrolled" if avg_tokens >= _dim128_unrolled_min_avg_tokens else "generic"
 
 
 def _binary_free_inputs(query, packed, offsets, dim, query_ndim):

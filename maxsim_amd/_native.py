@@ -30,6 +30,9 @@ SIGNATURES: dict[str, list] = {
     "msim_pack_int4": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp],
     "msim_pack_int4_async": [c_vp, c_i64, c_int, c_int, c_dbl, c_vp, c_vp, c_vp, c_vp, c_vp],
     "msim_get_fused_topk": [],
+    "msim_set_fused_wait_ticks": [c_i64],
+    "msim_get_fused_wait_ticks": [],
+    "msim_int4_fused_giveups": [c_vp, c_vp],
     "msim_set_scan_partition": [c_int],
     "msim_get_scan_partition": [],
     "msim_set_prefix_scan": [c_int],
@@ -90,7 +93,7 @@ SIGNATURES: dict[str, list] = {
     "msim_binary_cascade_topk_async": [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp],
 }
 
-_RESTYPES = {"msim_last_error": ctypes.c_char_p}
+_RESTYPES = {"msim_last_error": ctypes.c_char_p, "msim_get_fused_wait_ticks": c_i64}
 
 
 class Int4Props(ctypes.Structure):

@@ -27,7 +27,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from maxsim_amd._api import _as_numpy, _normalize_offsets
-from maxsim_amd.cascade import _stable_topk
+from maxsim_amd.cascade import DEVICE_TOPK_MAX_K, _stable_topk
 from maxsim_amd.experimental import pack_int4_symmetric
 
 
@@ -142,7 +142,9 @@ def _binres_topk(query_tokens, packed: BinaryResidualPackedDocs, k: int, *, quer
     selected on the device: the same result as the stable top-k of
     ``binres_score(...)`` without the [B, N] scores leaving the device."""
     q, squeeze = _query(query_tokens, packed.dim)
-    if q.shape[0] == 0 or q.shape[1] == 0:
+    if q.shape[0] == 0 or q.shape[1] == 0 or k > DEVICE_TOPK_MAX_K:
+        # Beyond the device selector's k: the stable top-k of the full fused
+        # score rows, as the reference's residual search selects.
         return _stable_topk(binres_score(query_tokens, packed, query_precision=query_precision), k)
     resident = binres_to_device(packed)
     with _RescorePrecision(resident.sign_data, query_precision):

@@ -160,6 +160,10 @@ def residual_score(query_tokens, packed: ResidualInt4PackedDocs, *, device: str 
     return result[0] if squeeze else result
 
 
+# Largest k the device selectors take (msim_*_topk_* entry points).
+DEVICE_TOPK_MAX_K = 4096
+
+
 def _residual_topk(query_tokens, packed: ResidualInt4PackedDocs, k: int, *, device: str = "auto",
                    reducer: str = "maxsim", query_weights=None, temperature: float = 1.0):
     """Top-k of the fused scores over every document, selected on the device:
@@ -170,7 +174,9 @@ def _residual_topk(query_tokens, packed: ResidualInt4PackedDocs, k: int, *, devi
     batches, squeeze = _normalize_query(query_tokens, packed.dim)
     reducer_value, weights, temperature_value = _normalize_reducer_options(
         reducer, query_weights, temperature, batch=batches.shape[0], query_tokens=batches.shape[1])
-    if batches.shape[0] == 0 or batches.shape[1] == 0:
+    if batches.shape[0] == 0 or batches.shape[1] == 0 or k > DEVICE_TOPK_MAX_K:
+        # Beyond the device selector's k: the reference's own route for this
+        # mode, the stable top-k of the full fused score rows (sdk.py:523-533).
         return _stable_topk(residual_score(query_tokens, packed, device=device, reducer=reducer,
                                            query_weights=query_weights, temperature=temperature), k)
     resident = _on_device(packed, device)

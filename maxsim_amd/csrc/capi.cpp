@@ -17,6 +17,7 @@ int g_docs_per_wave = 0;
 int g_fused_topk = 1;  // msim_set_fused_topk
 int g_scan_partition = 0;  // msim_set_scan_partition
 int g_scan_prefix = 1;     // msim_set_prefix_scan
+uint64_t g_fused_wait_ticks = kScanTailWaitTicks;  // msim_set_fused_wait_ticks
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -114,6 +115,15 @@ extern "C" int msim_set_fused_topk(int mode) {
 }
 
 extern "C" int msim_get_fused_topk(void) { return g_fused_topk; }
+
+extern "C" int msim_set_fused_wait_ticks(int64_t ticks) {
+  return guarded([&] {
+    if (ticks < 0) throw InvalidArgument("fused selection wait must be >= 0 ticks");
+    g_fused_wait_ticks = (uint64_t)ticks;
+  });
+}
+
+extern "C" int64_t msim_get_fused_wait_ticks(void) { return (int64_t)g_fused_wait_ticks; }
 
 extern "C" int msim_set_scan_partition(int mode) {
   return guarded([&] {
@@ -351,7 +361,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     // the key rows and workgroup records hold no tag of a later launch.
     if (h->tail_epoch.ptr == nullptr) {
       h->tail_epoch.ensure(256, "hipMalloc scan launch counter");
-      check_hip(launch_fill_f32(h->tail_epoch.as<float>(), 1, 0.0f, stream), "zero scan launch counter");
+      check_hip(launch_fill_f32(h->tail_epoch.as<float>(), 64, 0.0f, stream), "zero scan launch counters");
     }
     const int64_t rows = std::min(batch, std::max<int64_t>(1, kScanPassRows / query_tokens));
     const size_t key_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailRow);
@@ -370,6 +380,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     a.topk_k = (int32_t)k;
     a.tail_cap = g_fused_topk == 2 ? 0 : INT32_MAX;
     a.epoch = h->tail_epoch.as<uint32_t>();
+    a.tail_wait_ticks = g_fused_wait_ticks;
   }
   const int64_t per_pass = std::max<int64_t>(1, kScanPassRows / query_tokens);
   for (int64_t b0 = 0; b0 < batch; b0 += per_pass) {
@@ -416,6 +427,16 @@ void select_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, fl
 void run_int8q(msim_int4_docs* h, const float* d_query, int64_t batch, int64_t query_tokens,
                float* d_out, hipStream_t stream) {
   search_int8q(h, d_query, batch, query_tokens, d_out, 0, nullptr, nullptr, stream);
+}
+
+// A fused selection that gave up (its wait for the other workgroups ran out)
+// left id -1 in its row: a synchronous call reports it instead of returning it.
+void require_selected(const int64_t* ids, int64_t count) {
+  for (int64_t i = 0; i < count; ++i)
+    if (ids[i] < 0)
+      throw RuntimeError(
+          "int8q top-k: the fused selection gave up waiting for the scan's workgroups (device stalled or "
+          "oversubscribed); no result was returned");
 }
 
 float* ensure_scores(msim_int4_docs* h, int64_t batch, int64_t targets) {
@@ -594,8 +615,24 @@ extern "C" int msim_int4_topk_batch_int8q(msim_int4_docs* h, const float* query,
     float* d_scores = ensure_scores(h, batch, h->num_docs);
     search_int8q(h, reinterpret_cast<const float*>(io), batch, query_tokens, d_scores, k, h_top_s, h_top_i, stream);
     check_hip(hipStreamSynchronize(stream), "synchronize int8q topk kernels");
+    require_selected(h_top_i, batch * k);
     std::memcpy(out_scores, h_top_s, sbytes);
     std::memcpy(out_indices, h_top_i, ibytes);
+  });
+}
+
+extern "C" int msim_int4_fused_giveups(const msim_int4_docs* h, uint64_t* out) {
+  return guarded([&] {
+    require_handle(h);
+    if (out == nullptr) throw InvalidArgument("out pointer must not be NULL");
+    *out = 0;
+    if (h->tail_epoch.ptr == nullptr) return;
+    select_device(h->device);
+    uint32_t words[2] = {0, 0};
+    check_hip(hipDeviceSynchronize(), "synchronize before reading the fused selection counters");
+    check_hip(hipMemcpy(words, h->tail_epoch.ptr, sizeof(words), hipMemcpyDeviceToHost),
+              "copy fused selection counters to host");
+    *out = words[1];
   });
 }
 

@@ -578,7 +578,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   for (int b = wave; b < p.batch; b += kScanWaves)
     tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_rec + (int64_t)b * 3 * kScanTailBlocks, (int)gridDim.x,
               (int)p.num_docs, p.topk_k, p.tail_cap, tag, lds, bs, blen, p.top_scores + (int64_t)b * p.topk_k,
-              p.top_ids + (int64_t)b * p.topk_k);
+              p.top_ids + (int64_t)b * p.topk_k, p.tail_wait_ticks, p.epoch + 1);
   // Every workgroup read the counter at its start, before its block maxima
   // that the selection waited for: the next launch's tag can be published.
   if (threadIdx.x == 0) __hip_atomic_store(p.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

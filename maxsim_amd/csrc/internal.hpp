@@ -105,10 +105,14 @@ struct ScanArgs {
   // topk_k] and stores the tag to *epoch.  tail_keys and tail_rec hold no
   // entry with a later launch's tag (zero them when allocated).  block_pos
   // [num_waves / 4 + 1] holds each workgroup's first position (then num_docs).
+  // A selection that waits longer than tail_wait_ticks (s_memrealtime ticks,
+  // 100 MHz; 0 = give up at once) writes id -1 / NaN to its batch row and adds
+  // one to epoch[1].
   int32_t topk_k;
   int32_t tail_cap;             // 0 forces the selection's k-round path
   int64_t num_docs;
-  uint32_t* epoch;
+  uint32_t* epoch;              // [0]: launch counter, [1]: selections given up
+  uint64_t tail_wait_ticks;
   float* top_scores;
   int64_t* top_ids;
   uint64_t* tail_keys;
@@ -121,6 +125,7 @@ constexpr int64_t kScanTailMinDocs = 256;  // every lane of the selecting wave h
 constexpr int64_t kScanTailRow = 4096;  // key positions per batch row of the fused selection
 constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
 constexpr int kScanTailBlocks = 512;  // workgroups of a fused launch at most
+constexpr uint64_t kScanTailWaitTicks = 10000000;  // default wait of the fused selection: 100 ms
 // Epilogue forms of the scan (the token scales decide which is exact):
 //  * kScanEpiIntMax: tensor-scale corpora (token_scale16 == nullptr): integer
 //    maximum of the dots, scaled at the document end;

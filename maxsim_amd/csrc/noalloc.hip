@@ -106,6 +106,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
       a.topk_k = (int32_t)k;
       a.tail_cap = mode == 2 ? 0 : INT32_MAX;
       a.epoch = reinterpret_cast<uint32_t*>(base + kEpochOff);
+      a.tail_wait_ticks = msim_get_fused_wait_ticks();
       a.top_scores = d_scores;
       a.top_ids = d_indices;
     }

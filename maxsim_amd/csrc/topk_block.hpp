@@ -422,9 +422,10 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // Every entry carries the launch's tag (rec[2]: its low 32 bits, full keys:
 // their low kTailTagBits bits, tail_key_tag), and the selection reads an
 // entry again until it carries the tag: stores of other workgroups are in
-// flight, not missing, so the wait is short; a wait longer than
-// kTailWaitTicks (an unusable device) ends it with id -1 and a NaN score in
-// every output slot of the row.
+// flight, not missing, so the wait is short.  A wait longer than the
+// caller's budget (wait_ticks of s_memrealtime; 0 = no read at all) gives up:
+// id -1 and a NaN score in every output slot of the row, and one is added to
+// *status, so that the host can tell a given-up row from a result.
 //
 // Keys: tail_key maps a float's bits to a 32-bit order-preserving key (u ^
 // 2^31 for sign bit 0, -u otherwise, so -0 ties +0; every finite float's key
@@ -452,7 +453,6 @@ constexpr int kTailBlockKeys = 16;                          // documents per dee
 constexpr int kTailMaxDocs = 4096;                          // ids below 2^12
 constexpr int kTailTagBits = 19;
 constexpr uint32_t kTailTagMask = (1u << kTailTagBits) - 1u;
-constexpr uint64_t kTailWaitTicks = 10000000;               // 100 ms of s_memrealtime (100 MHz)
 // LDS of the selecting wave: candidates (at most kTailBlockKeys per hot
 // block, then eight zero keys), then the list of deep blocks.
 constexpr int kTailCandMax = kTailHotMax * kTailBlockKeys;
@@ -514,7 +514,8 @@ __device__ __forceinline__ void tail_block_ranges(const int64_t* bpos, int nbloc
 __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64_t* rec_arg, int nblocks_arg,
                                           int n_arg, int k_arg, int cap_arg, uint32_t tag_arg, uint64_t* lds_arg,
                                           const int (&bs)[kTailBlocksPerLane], const int (&len)[kTailBlocksPerLane],
-                                          float* out_s_arg, int64_t* out_i_arg) {
+                                          float* out_s_arg, int64_t* out_i_arg, uint64_t wait_ticks,
+                                          uint32_t* status) {
   const uint64_t* keys = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(keys_arg)));
   const uint64_t* rec = reinterpret_cast<const uint64_t*>(wave_uniform64(reinterpret_cast<int64_t>(rec_arg)));
   float* out_s = reinterpret_cast<float*>(wave_uniform64(reinterpret_cast<int64_t>(out_s_arg)));
@@ -530,13 +531,18 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   const int lane = lane_id();
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys, (uint32_t)n * 8u);
   const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-  auto expired = [&]() { return __builtin_amdgcn_s_memrealtime() - t_start > kTailWaitTicks; };
+  auto expired = [&]() { return __builtin_amdgcn_s_memrealtime() - t_start > wait_ticks; };
   auto give_up = [&]() {
     if (lane < k) {
       out_s[lane] = __uint_as_float(0x7FC00000u);  // quiet NaN by its bits (device code is built without NaN semantics)
       out_i[lane] = -1;
     }
+    if (lane == 0) __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
+  if (wait_ticks == 0) {
+    give_up();
+    return;
+  }
   auto rank_below = [&](uint64_t mask) -> int {  // set bits of mask below this lane
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
   };

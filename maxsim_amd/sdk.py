@@ -14,7 +14,8 @@ prefix with a per-token scale + per-token int4 residual; see
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Any, Literal
 
 import numpy as np
@@ -67,6 +68,18 @@ def resolve_auto_mode(num_docs: int, embeddings: np.ndarray | None = None) -> st
 
 
 @dataclass(frozen=True)
+class CorpusMemoryReport:
+    """Byte counts of an encoded corpus and of its current residency
+    (reference: CorpusMemoryReport, sdk.py:62-70)."""
+
+    encoded_bytes: int
+    host_array_bytes: int
+    device_index_bytes: int
+    device_workspace_bytes: int | None
+    serialized_bytes: int | None
+
+
+@dataclass(frozen=True)
 class SearchResult:
     doc_id: str
     score: float
@@ -83,6 +96,7 @@ class Corpus:
     int4_packed: object | None = None
     calibration: object | None = None
     metadata: dict[str, Any] | None = None
+    _source_path: Path | None = field(default=None, repr=False, compare=False)
 
     @classmethod
     def from_embeddings(cls, doc_ids, embeddings, offsets, *, mode: str = "auto", pool_factor: int | None = None,
@@ -163,14 +177,34 @@ class Corpus:
         """Write the reference's .npz index format (sdk.py:203-288)."""
         from maxsim_amd.index_io import save_corpus
 
-        save_corpus(self, path)
+        written = save_corpus(self, path)
+        object.__setattr__(self, "_source_path", Path(written).resolve())
 
     @classmethod
     def load(cls, path) -> "Corpus":
         """Read a .npz index of schema version 1 or 2 (sdk.py:290-410)."""
         from maxsim_amd.index_io import load_corpus
 
-        return load_corpus(path)
+        corpus = load_corpus(path)
+        object.__setattr__(corpus, "_source_path", Path(path).resolve())
+        return corpus
+
+    def memory_report(self, serialized_path=None) -> CorpusMemoryReport:
+        """Logical size and current host / device residency (sdk.py:453-469).
+
+        host_array_bytes counts the NumPy buffers the corpus owns (not Python
+        object overhead); the device figures come from the resident handle's
+        resident_bytes / workspace_bytes (0 for a host corpus);
+        serialized_bytes is the size of the index file this corpus was saved
+        to or loaded from, or of ``serialized_path``, else None."""
+        source = self._source_path if serialized_path is None else Path(serialized_path)
+        return CorpusMemoryReport(
+            encoded_bytes=self.encoded_bytes,
+            host_array_bytes=_corpus_host_array_bytes(self),
+            device_index_bytes=_corpus_device_bytes(self, "resident_bytes"),
+            device_workspace_bytes=_corpus_device_bytes(self, "workspace_bytes"),
+            serialized_bytes=None if source is None else int(source.stat().st_size),
+        )
 
 
 Index = Corpus
@@ -276,20 +310,66 @@ class Reranker:
         return np.asarray(out, dtype=np.int64)
 
 
+# NumPy fields of each payload type that a memory report counts
+# (sdk.py:944-984 lists the reference's own payloads the same way).
+_HOST_ARRAY_FIELDS = {
+    "packed": ("data", "doc_offsets", "scale", "token_scale"),
+    "int4": ("data", "values", "doc_offsets", "token_scale"),
+    "int4_residual": ("prefix_data", "prefix_values", "prefix_token_scale", "residual_data", "residual_values",
+                      "residual_token_scale", "doc_offsets"),
+    "binary_residual": ("sign_data", "prefix_scale", "residual_data", "residual_values", "residual_token_scale",
+                        "doc_offsets"),
+}
+
+
+def _corpus_payload(corpus: Corpus):
+    """(payload, kind, device handle attribute) of a corpus."""
+    if corpus.packed is not None:
+        return corpus.packed, "packed", "data"
+    if corpus.mode == "int4_residual":
+        return corpus.int4_packed, "int4_residual", "prefix_data"
+    if isinstance(corpus.int4_packed, BinaryResidualPackedDocs):
+        return corpus.int4_packed, "binary_residual", "sign_data"
+    return corpus.int4_packed, "int4", "data"
+
+
+def _corpus_host_array_bytes(corpus: Corpus) -> int:
+    payload, kind, _ = _corpus_payload(corpus)
+    total = 0
+    if payload is not None:
+        for name in _HOST_ARRAY_FIELDS[kind]:
+            value = getattr(payload, name, None)
+            if isinstance(value, np.ndarray):
+                total += int(value.nbytes)
+    if corpus.calibration is not None:
+        for name in ("thresholds", "negative_centroids", "positive_centroids"):
+            value = getattr(corpus.calibration, name, None)
+            if isinstance(value, np.ndarray):
+                total += int(value.nbytes)
+    return total
+
+
+def _corpus_device_bytes(corpus: Corpus, accessor: str) -> int:
+    payload, _, handle_name = _corpus_payload(corpus)
+    if payload is None or getattr(payload, "device", "cpu") != "cuda":
+        return 0
+    return int(getattr(getattr(payload, handle_name), accessor))
+
+
 def _move_corpus(corpus: Corpus) -> Corpus:
     """Resident copy of the corpus (sdk.py:1011-1045)."""
     if corpus.packed is not None:
         return Corpus(corpus.doc_ids, corpus.mode, to_device(corpus.packed, "cuda"), corpus.int4_packed,
-                      corpus.calibration, corpus.metadata)
+                      corpus.calibration, corpus.metadata, corpus._source_path)
     if corpus.mode == "int4_residual":
         return Corpus(corpus.doc_ids, corpus.mode, None, residual_int4_to_device(corpus.int4_packed),
-                      corpus.calibration, corpus.metadata)
+                      corpus.calibration, corpus.metadata, corpus._source_path)
     if isinstance(corpus.int4_packed, BinaryResidualPackedDocs):
         return Corpus(corpus.doc_ids, corpus.mode, None, binres_to_device(corpus.int4_packed), corpus.calibration,
-                      corpus.metadata)
+                      corpus.metadata, corpus._source_path)
     if corpus.int4_packed is not None:
         return Corpus(corpus.doc_ids, corpus.mode, None, int4_to_device(corpus.int4_packed), corpus.calibration,
-                      corpus.metadata)
+                      corpus.metadata, corpus._source_path)
     return corpus
 
 
@@ -363,6 +443,8 @@ def _dedupe_candidate_ids(candidate_ids) -> tuple[str, ...]:
 def _format_topk_results(scores, indices, doc_ids):
     s = np.asarray(scores, dtype=np.float32)
     i = np.asarray(indices, dtype=np.int64)
+    if i.size and int(i.min()) < 0:
+        raise RuntimeError("top-k selection returned no document for some rank (a device selection gave up)")
     # Python floats and ints once per array (tolist), not per numpy scalar.
     if s.ndim == 1:
         return _format_result_row(s.tolist(), i.tolist(), doc_ids)

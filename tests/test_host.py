@@ -295,3 +295,72 @@ def test_maxsim_cuda_batch_requires_3d_query():
 
     with pytest.raises(ValueError, match=r"query must have shape \[batch, query_tokens, dim\]"):
         _maxsim_hip.maxsim_cuda_batch(np.zeros((2, 8), np.float32), np.zeros((3, 1), np.uint8), [0, 3], 8)
+
+
+def test_reference_routing_knobs_validate_like_the_reference():
+    """The reference module's launch-shape knobs (cuda_extension.cu:3482-3513):
+    same defaults, accepted values and ValueError texts; a rejected value
+    leaves the setting unchanged (tests/test_cuda_reducers.py:519-528)."""
+    from maxsim_amd import _maxsim_hip as h
+
+    assert (h.get_shared_reducer_warps(), h.get_residual_reducer_warps(), h.get_residual_reducer_force_warps()) == (
+        4, 8, -1)
+    assert h.get_dim128_unrolled_min_avg_tokens() == 256
+    assert h.get_dim128_qtile_min_packed_bytes() == 2**64 - 1
+    for setter, getter, good, bad, msg in [
+        (h.set_shared_reducer_warps, h.get_shared_reducer_warps, (0, 4, 8), (-1, 1, 2, 16), "one of 0, 4, or 8"),
+        (h.set_residual_reducer_warps, h.get_residual_reducer_warps, (0, 4, 8), (-1, 1, 2, 16), "one of 0, 4, or 8"),
+        (h.set_residual_reducer_force_warps, h.get_residual_reducer_force_warps, (-1, 0, 4, 8), (-2, 1, 16),
+         "one of -1, 0, 4, or 8"),
+    ]:
+        prior = getter()
+        try:
+            for v in good:
+                setter(v)
+                assert getter() == v
+            for v in bad:
+                before = getter()
+                with pytest.raises(ValueError, match=msg):
+                    setter(v)
+                assert getter() == before
+        finally:
+            setter(prior)
+    # The residual policy of cu:58-76.
+    prior = (h.get_residual_reducer_warps(), h.get_residual_reducer_force_warps())
+    try:
+        assert [h.get_effective_residual_reducer_warps(q) for q in (1, 7, 8, 32)] == [4, 4, 8, 8]
+        h.set_residual_reducer_warps(4)
+        assert [h.get_effective_residual_reducer_warps(q) for q in (1, 3, 4, 32)] == [0, 0, 4, 4]
+        h.set_residual_reducer_force_warps(0)
+        assert h.get_effective_residual_reducer_warps(32) == 0
+        with pytest.raises(ValueError, match="query tokens must be positive"):
+            h.get_effective_residual_reducer_warps(0)
+    finally:
+        h.set_residual_reducer_warps(prior[0])
+        h.set_residual_reducer_force_warps(prior[1])
+    prior_q = h.get_dim128_qtile_min_packed_bytes()
+    try:
+        h.set_dim128_qtile_min_packed_bytes(1 << 62)
+        assert h.get_dim128_qtile_min_packed_bytes() == 1 << 62
+        with pytest.raises(TypeError):
+            h.set_dim128_qtile_min_packed_bytes(-1)
+    finally:
+        h.set_dim128_qtile_min_packed_bytes(prior_q)
+
+
+def test_routing_knobs_are_per_thread_like_the_reference():
+    """The warp knobs are thread_local in the reference (cu:44-56)."""
+    import threading
+
+    from maxsim_amd import _maxsim_hip as h
+
+    prior = h.get_shared_reducer_warps()
+    seen = []
+    try:
+        h.set_shared_reducer_warps(8)
+        t = threading.Thread(target=lambda: seen.append(h.get_shared_reducer_warps()))
+        t.start()
+        t.join()
+        assert seen == [4] and h.get_shared_reducer_warps() == 8
+    finally:
+        h.set_shared_reducer_warps(prior)

@@ -181,3 +181,65 @@ def test_save_rejects_invalid_payloads(tmp_path):
                                 dim=packed.dim, num_docs=packed.num_docs)
     with pytest.raises(ValueError, match="monotonically"):
         maxsim.Corpus(doc_ids=("a", "b", "c"), mode="binary", packed=invalid).save(tmp_path / "y.npz")
+
+
+def _report_docs():
+    rng = np.random.default_rng(382)
+    docs = rng.standard_normal((11, 16)).astype(np.float32)
+    return docs, np.array([0, 4, 7, 11], dtype=np.int64)
+
+
+def test_memory_report_counts_encoded_host_and_serialized_bytes(tmp_path):
+    """tests/test_sdk.py:382-408: host bytes are the payload's NumPy buffers;
+    serialized bytes follow save / load / an explicit path."""
+    docs, offsets = _report_docs()
+    corpus = maxsim.Corpus.from_embeddings(["a", "b", "c"], docs, offsets, mode="int4_per_token")
+    report = corpus.memory_report()
+    p = corpus.int4_packed
+    assert isinstance(report, maxsim.CorpusMemoryReport)
+    assert report.encoded_bytes == corpus.storage_bytes
+    assert report.host_array_bytes == p.data.nbytes + p.values.nbytes + p.doc_offsets.nbytes + p.token_scale.nbytes
+    assert (report.device_index_bytes, report.device_workspace_bytes, report.serialized_bytes) == (0, 0, None)
+    path = tmp_path / "memory.maxsim.npz"
+    corpus.save(path)
+    size = path.stat().st_size
+    assert corpus.memory_report().serialized_bytes == size
+    assert corpus.memory_report(path).serialized_bytes == size
+    assert maxsim.Corpus.load(path).memory_report().serialized_bytes == size
+
+
+def test_memory_report_path_without_npz_suffix(tmp_path):
+    """tests/test_sdk.py:411-426."""
+    docs, offsets = _report_docs()
+    corpus = maxsim.Corpus.from_embeddings(["a", "b", "c"], docs, offsets, mode="int4_per_token")
+    path = tmp_path / "corpus.index"
+    corpus.save(path)
+    assert path.is_file() and not path.with_suffix(path.suffix + ".npz").exists()
+    assert corpus.memory_report().serialized_bytes == path.stat().st_size
+
+
+def test_memory_report_reads_the_device_handle_accessors():
+    """tests/test_sdk.py:429-450: a resident payload reports its handle's
+    resident_bytes and workspace_bytes."""
+
+    class FakeHandle:
+        dim = 8
+        num_docs = 3
+        packed_size = 3
+        resident_bytes = 91
+        workspace_bytes = 37
+
+    packed = maxsim.PackedDocs(data=FakeHandle(), doc_offsets=np.array([0, 1, 2, 3], dtype=np.int64), dim=8,
+                               num_docs=3, device="cuda")
+    report = maxsim.Corpus(doc_ids=("a", "b", "c"), mode="binary", packed=packed).memory_report()
+    assert report.host_array_bytes == packed.doc_offsets.nbytes
+    assert (report.device_index_bytes, report.device_workspace_bytes) == (91, 37)
+
+
+@pytest.mark.parametrize("mode", ["binary", "binary_token_scale", "int4", "int4_residual", "binary_residual"])
+def test_memory_report_host_bytes_every_mode(mode):
+    docs, offsets = _report_docs()
+    corpus = maxsim.Corpus.from_embeddings(["a", "b", "c"], docs, offsets, mode=mode)
+    payload = corpus.packed if corpus.packed is not None else corpus.int4_packed
+    arrays = [v for v in vars(payload).values() if isinstance(v, np.ndarray)]
+    assert corpus.memory_report().host_array_bytes == sum(a.nbytes for a in arrays)

@@ -1,7 +1,8 @@
 """GPU test of msim_int4_topk_int8q_noalloc, called through the C ABI: its
-top-k equals msim_int4_topk_int8q_async's bit for bit on two calls in a row,
-the second with a smaller input, and the call allocates nothing (the handle's
-workspace, torch's allocations and the device's free memory stay as they were).
+top-k equals msim_int4_topk_int8q_async's bit for bit, and the C oracle's
+stable top-k of its int8-query scores, on two calls in a row, the second with
+a smaller input, and the call allocates nothing (the handle's workspace,
+torch's allocations and the device's free memory stay as they were).
 """
 import ctypes
 
@@ -24,7 +25,7 @@ def _setup(n, lo, hi, batch, qtok, seed, gran="token"):
     handle = int4_to_device(packed).data
     rng = np.random.default_rng(seed + 1)
     query = torch.from_numpy(rng.standard_normal((batch, qtok, 128)).astype(np.float32)).cuda()
-    return handle, query
+    return handle, query, packed
 
 
 def _workspace_bytes(lib, handle):
@@ -52,7 +53,7 @@ def _run(lib, entry, handle, query, k, scores, ids):
     return scores.cpu().numpy(), ids.cpu().numpy()
 
 
-def _compare(lib, handle, query, k):
+def _compare(lib, handle, query, k, oracle=None, packed=None):
     import torch
 
     batch = query.shape[0]
@@ -69,6 +70,12 @@ def _compare(lib, handle, query, k):
     ref_s, ref_i = _run(lib, "msim_int4_topk_int8q_async", handle, query, k, scores, ids)
     np.testing.assert_array_equal(got_i, ref_i)
     np.testing.assert_array_equal(got_s.view(np.uint32), ref_s.view(np.uint32))
+    if oracle is not None:
+        exp = oracle.int4_int8q_scores(query.cpu().numpy(), packed.values, packed.doc_offsets,
+                                       token_scale=packed.token_scale, scale=float(packed.scale))
+        orc_s, orc_i = oracle.topk(exp, k)
+        np.testing.assert_array_equal(got_i, orc_i)
+        np.testing.assert_array_equal(got_s.view(np.uint32), orc_s.view(np.uint32))
 
 
 @pytest.fixture
@@ -82,43 +89,44 @@ PAIRS = [
     ((4096, 64, 192, 4, 32, 10, "token"), (1500, 8, 40, 2, 16, 7, "token")),   # config-2 shape, then smaller
     ((3000, 0, 60, 8, 16, 32, "tensor"), (300, 0, 20, 3, 8, 5, "tensor")),    # 8 batch rows, k at its limit
     ((900, 1, 30, 2, 64, 12, "token"), (100, 1, 10, 1, 32, 3, "token")),      # second call below 256 docs
+    ((4096, 16, 64, 8, 16, 32, "token"), (2000, 4, 30, 5, 16, 9, "token")),   # the fused limits: 8 rows, 4096 docs, k 32
 ]
 
 
 @pytest.mark.parametrize("mode", [1, 2, 0])
-@pytest.mark.parametrize("pair", PAIRS, ids=["config2_then_small", "b8_then_small", "then_lt256"])
-def test_noalloc_matches_async(gpu, fused_mode, mode, pair):
+@pytest.mark.parametrize("pair", PAIRS, ids=["config2_then_small", "b8_then_small", "then_lt256", "limits_then_small"])
+def test_noalloc_matches_async(gpu, oracle, fused_mode, mode, pair):
     import torch
 
     fused_mode(mode)
     # The first call on the device looks the scratch array up (its code object
     # may load then): make one before any memory is compared.
-    handle, query = _setup(300, 1, 4, 1, 1, seed=3)
+    handle, query, _ = _setup(300, 1, 4, 1, 1, seed=3)
     out_s = torch.empty((1, 1), device="cuda")
     out_i = torch.empty((1, 1), dtype=torch.int64, device="cuda")
     _run(gpu, "msim_int4_topk_int8q_noalloc", handle, query, 1, out_s, out_i)
     for i, (n, lo, hi, b, q, k, gran) in enumerate(pair):
         print(f"noalloc mode={mode} call={i} n={n} B={b} Q={q} k={k} {gran}", flush=True)
-        handle, query = _setup(n, lo, hi, b, q, seed=7 * n + q, gran=gran)
-        _compare(gpu, handle, query, k)
+        handle, query, packed = _setup(n, lo, hi, b, q, seed=7 * n + q, gran=gran)
+        _compare(gpu, handle, query, k, oracle, packed)
 
 
-def test_noalloc_same_handle_shrinking_batch(gpu):
+def test_noalloc_same_handle_shrinking_batch(gpu, oracle):
     import torch
 
-    handle, query = _setup(2048, 16, 80, 4, 32, seed=11)
+    handle, query, packed = _setup(2048, 16, 80, 4, 32, seed=11)
     out_s = torch.empty((4, 10), device="cuda")
     out_i = torch.empty((4, 10), dtype=torch.int64, device="cuda")
     _run(gpu, "msim_int4_topk_int8q_noalloc", handle, query, 10, out_s, out_i)
     print("noalloc same handle B=4 then B=1", flush=True)
     _compare(gpu, handle, query, 10)
-    _compare(gpu, handle, query[:1].contiguous(), 10)
+    _compare(gpu, handle, query[:1].contiguous(), 10, oracle, packed)
 
 
 def test_noalloc_rejects_sizes_beyond_its_limits(gpu):
     import torch
 
-    handle, query = _setup(5000, 1, 6, 2, 32, seed=5)
+    handle, query, _ = _setup(5000, 1, 6, 2, 32, seed=5)
     print("noalloc limits", flush=True)
     scores = torch.empty((8, 64), device="cuda")
     ids = torch.empty((8, 64), dtype=torch.int64, device="cuda")
