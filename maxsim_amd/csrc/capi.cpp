@@ -162,12 +162,13 @@ void check_int8q(const msim_int4_docs* h) {
   if (h->dim != 128) throw InvalidArgument("int8 query scoring currently requires dim=128");
 }
 
-// Upload `count` floats times `factor` (a power of two: exact).
+// Upload `count` floats times `factor` (a power of two: exact), followed by
+// kScanPadTokens zeros (the scan's loads may read that far past the end).
 void upload_scaled(DeviceBuffer& dst, const float* src, int64_t count, float factor, const char* what) {
-  std::vector<float> scaled(src, src + count);
-  for (float& v : scaled) v *= factor;
-  dst.ensure(std::max<int64_t>(count * 4, 4), what);
-  if (count) check_hip(hipMemcpy(dst.ptr, scaled.data(), count * 4, hipMemcpyHostToDevice), what);
+  std::vector<float> scaled((size_t)(count + kScanPadTokens), 0.0f);
+  for (int64_t i = 0; i < count; ++i) scaled[(size_t)i] = src[i] * factor;
+  dst.ensure(scaled.size() * 4, what);
+  check_hip(hipMemcpy(dst.ptr, scaled.data(), scaled.size() * 4, hipMemcpyHostToDevice), what);
 }
 
 // int4 rows of row_bytes < 64 bytes widened to 64 bytes with zero nibbles
@@ -470,10 +471,14 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
     h->host_offsets.assign(offsets, offsets + num_offsets);
     for (int64_t d = 0; d + 1 < num_offsets; ++d)
       h->max_doc_tiles = std::max<int64_t>(h->max_doc_tiles, (offsets[d + 1] - offsets[d] + 15) / 16);
-    h->packed.ensure(std::max<uint64_t>(h->packed_size, 64), "hipMalloc int4 packed docs");
+    // kScanPadTokens zero tokens follow the corpus (the scan's loads may read
+    // that far past the end).
+    const uint64_t pad_bytes = (uint64_t)kScanPadTokens * (uint64_t)row_bytes;
+    h->packed.ensure(std::max<uint64_t>(h->packed_size + pad_bytes, 64), "hipMalloc int4 packed docs");
     h->offsets.ensure(h->offsets_size * 8, "hipMalloc int4 offsets");
     if (h->packed_size)
       check_hip(hipMemcpy(h->packed.ptr, packed, h->packed_size, hipMemcpyHostToDevice), "copy int4 packed docs to device");
+    check_hip(hipMemset(h->packed.as<uint8_t>() + h->packed_size, 0, pad_bytes), "zero int4 packed docs padding");
     check_hip(hipMemcpy(h->offsets.ptr, offsets, h->offsets_size * 8, hipMemcpyHostToDevice), "copy int4 offsets to device");
     if (dim < 128) upload_codes128(h->codes128, packed, num_tokens, row_bytes, "int4 packed docs (128 dims)");
     // The int8-query scan's tables, built here so that the first search (and
@@ -497,9 +502,7 @@ extern "C" int msim_int4_set_token_scale(msim_int4_docs* h, const float* token_s
     if (count != h->num_tokens) throw InvalidArgument("token scale vector must have shape [num_doc_tokens]");
     validate_positive_scales(token_scales, count, "token scales must be finite and > 0");
     select_device(h->device);
-    h->token_scales.ensure(std::max<int64_t>(count * 4, 4), "hipMalloc resident int4 token scale vector");
-    if (count)
-      check_hip(hipMemcpy(h->token_scales.ptr, token_scales, count * 4, hipMemcpyHostToDevice), "copy int4 token scale vector to device");
+    upload_scaled(h->token_scales, token_scales, count, 1.0f, "int4 token scale vector");
     // The MFMA kernels multiply 16 * dot by s / 16 (a power-of-two rescale,
     // exact for normal floats).
     upload_scaled(h->token_scales16, token_scales, count, 0.0625f, "int4 token scale vector / 16");

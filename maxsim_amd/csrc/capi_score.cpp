@@ -10,6 +10,8 @@
 
 #include "capi_handles.hpp"
 
+#include <algorithm>
+
 namespace msim {
 
 namespace {
@@ -520,8 +522,10 @@ extern "C" int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int
     h->host_offsets.assign(offsets, offsets + num_offsets);
     for (int64_t d = 0; d + 1 < num_offsets; ++d)
       h->max_doc_tiles = std::max<int64_t>(h->max_doc_tiles, (offsets[d + 1] - offsets[d] + 15) / 16);
-    // Rows widened to 16 bytes: padding bits meet zero query dims.
-    std::vector<uint8_t> wide((size_t)std::max<int64_t>(num_tokens, 1) * 16, 0);
+    // Rows widened to 16 bytes: padding bits meet zero query dims.  The
+    // int8-query scan of the sign stream may read kScanPadTokens rows past
+    // the end: zero rows follow.
+    std::vector<uint8_t> wide((size_t)(num_tokens + kScanPadTokens) * 16, 0);
     for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 16], packed + t * row_bytes, (size_t)row_bytes);
     upload_vec(h->packed, wide, "copy binary packed docs to device");
     std::vector<int64_t> offs(offsets, offsets + num_offsets);
@@ -561,11 +565,12 @@ extern "C" int msim_binary_set_token_scale(msim_binary_docs* h, const float* tok
     require_handle(h);
     if (count != h->num_tokens) throw InvalidArgument("token scale vector must have shape [num_doc_tokens]");
     select_device(h->device);
+    h->token_scales_fma = std::all_of(token_scales, token_scales + count,
+                                      [](float x) { return x >= kScanFmaMinScale && x < kScanFmaMaxScale; });
     std::vector<float> v(token_scales, token_scales + count);
+    v.resize((size_t)(count + kScanPadTokens), 0.0f);  // rows the scan may read past the end
     upload_vec(h->token_scales, v, "copy binary token scale vector to device");
     h->has_token_scale = true;
-    h->token_scales_fma = true;
-    for (float x : v) h->token_scales_fma = h->token_scales_fma && x >= kScanFmaMinScale && x < kScanFmaMaxScale;
   });
 }
 

@@ -82,6 +82,26 @@ __device__ __forceinline__ void lds_load_b32(v4i rsrc, uint32_t byte_offset, uin
       : "memory");
 }
 
+// The same with a wave-uniform byte offset (soffset) added to every lane's
+// voffset.  The buffer range check covers voffset only: the caller keeps
+// soffset + voffset inside the buffer.
+__device__ __forceinline__ void lds_load_b128_so(v4i rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+      : "memory");
+}
+__device__ __forceinline__ void lds_load_b32_so(v4i rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %2, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+      : "memory");
+}
+
 // A use of `v` at this point: the compiler completes its load here.
 template <typename T>
 __device__ __forceinline__ void use_here(const T& v) {

@@ -49,7 +49,7 @@ static_assert(kScanTailBlocks == kTailBlocks && kScanTailMaxDocs <= kScanTailRow
               "fused selection sizes");
 static_assert(kScanTailMaxRows <= kScanThreads, "one thread per batch row writes the block maxima");
 static_assert(kPrefetch * kWave * 16 >= kTailLdsBytes, "a wave's tile ring holds the selection's candidates");
-static_assert(kScanTailMaxK <= kWave, "fused selection k");
+static_assert(kScanTailMaxK <= 32, "fused selection k: the selection's list holds 32 keys");
 
 // Maximum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48).
 __device__ __forceinline__ float max_over_groups(float v) {
@@ -233,12 +233,13 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     }
   }
 
-  // Bounds-checked descriptors over the wave's tokens (rows past the wave
-  // read zero).
+  // Descriptors over the wave's tokens and the kScanPadTokens zero rows that
+  // follow the corpus (tile starts are wave-relative and below T1 - T0, so
+  // every tile's 16 rows lie in that range).
   constexpr int kTokenBytes = kSign ? 16 : 64;
-  const v4i rc = make_rsrc_words(codes + T0 * kTokenBytes, (uint32_t)((T1 - T0) * kTokenBytes));
+  const v4i rc = make_rsrc_words(codes + T0 * kTokenBytes, (uint32_t)((T1 - T0 + kScanPadTokens) * kTokenBytes));
   const v4i rs = make_rsrc_words(kTS ? (const void*)(token_scale16 + T0) : (const void*)codes,
-                                 kTS ? (uint32_t)((T1 - T0) * 4) : 0u);
+                                 kTS ? (uint32_t)((T1 - T0 + kScanPadTokens) * 4) : 0u);
   const uint32_t ring_codes = wave_uniform((int)lds_address(&s_codes[wave][0][0]));
   const uint32_t ring_scales = wave_uniform((int)lds_address(&s_scales[wave][0][0]));
 
@@ -247,14 +248,19 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // last one at e - 16.  Lane (g, c) fetches the 16 code bytes of token
   // t + c for dims [32g, 32g + 32) and the (pre-divided by 16) scale of
   // token t + c; a lane then reads the four scales of its accumulator rows
-  // 4g..4g+3 as one 16-byte LDS read.  Every step issues exactly kOps loads,
-  // so slot i is complete once vmcnt <= (kPrefetch - 1) * kOps.
+  // 4g..4g+3 as one 16-byte LDS read.  The tile's byte offset is the loads'
+  // scalar offset, the lane's part a constant VGPR.  Every step issues
+  // exactly kOps loads, so slot i is complete once vmcnt <= (kPrefetch - 1) *
+  // kOps.
   constexpr int kOps = kTS ? 2 : 1;
   constexpr int kRingWait = (kPrefetch - 1) * kOps;
+  const uint32_t voff_codes = kSign ? 16u * (uint32_t)c + 4u * (uint32_t)g : 64u * (uint32_t)c + 16u * (uint32_t)g;
+  const uint32_t voff_scales = 4u * (uint32_t)c;
   auto load_tile = [&](int slot_, uint32_t t) {
-    if (kSign) lds_load_b32(rc, (t + (uint32_t)c) * 16u + 4u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
-    else lds_load_b128(rc, (t + (uint32_t)c) * 64u + 16u * (uint32_t)g, ring_codes + slot_ * kWave * 16);
-    if (kTS) lds_load_b32(rs, (t + (uint32_t)c) * 4u, ring_scales + slot_ * kWave * 4);
+    const uint32_t tu = (uint32_t)wave_uniform((int)t);
+    if (kSign) lds_load_b32_so(rc, voff_codes, tu * 16u, ring_codes + slot_ * kWave * 16);
+    else lds_load_b128_so(rc, voff_codes, tu * 64u, ring_codes + slot_ * kWave * 16);
+    if (kTS) lds_load_b32_so(rs, voff_scales, tu * 4u, ring_scales + slot_ * kWave * 4);
   };
 #pragma unroll
   for (int s = 0; s < kPrefetch; ++s) load_tile(s, (uint32_t)tt[s]);
@@ -299,9 +305,13 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // bits 32..36 as rows - 1) and its four token scales.  Rows past a short
   // document are masked: -inf for the scaled forms (c = -inf, or a = +inf on
   // an accumulator starting at -2^30), a -2^30 start for the integer form.
+  // The kScanEpiFma C operand, kept in registers for the whole loop (an
+  // opaque copy: rebuilding it from a constant would take two moves per tile).
+  v4i cmagic = (v4i){kMagic, kMagic, kMagic, kMagic};
+  if (EPI == kScanEpiFma) asm volatile("" : "+v"(cmagic));
   auto prep = [&](uint32_t mhi, const v4u& sv, TileEpi& e) -> v4i {
     const uint32_t rows = (mhi & 31u) + 1u;
-    v4i cinit = EPI == kScanEpiFma ? (v4i){kMagic, kMagic, kMagic, kMagic} : (v4i){0, 0, 0, 0};
+    v4i cinit = EPI == kScanEpiFma ? cmagic : (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       e.a[r] = kTS ? __uint_as_float(sv[r]) : 1.0f;

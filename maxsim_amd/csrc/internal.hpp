@@ -58,9 +58,14 @@ hipError_t launch_int8q_finish(const float* d_rowmax, const float* d_qscale, int
 //                   follows the num_waves rows in the same buffer
 // The table is padded to whole workgroups with waves of no tiles.  Tile table
 // entries (one per tile, then kScanPrefetch + 1 padding entries per wave):
-// low 32 bits the tile's first token relative to T0 (kScanPastEnd for
-// padding), then (rows - 1) in bits 32..36, "last tile of its document" in
-// bit 37 and the document's index relative to d0 in bits 40..63.
+// low 32 bits the tile's first token relative to T0 (0 for padding: the
+// prefetch of a padding entry reads the wave's first tokens again), then
+// (rows - 1) in bits 32..36, "last tile of its document" in bit 37 and the
+// document's index relative to d0 in bits 40..63.  The kernel adds a tile's
+// byte offset to its loads outside the buffer range check (soffset), so every
+// address it forms must lie in the corpus buffers: they hold kScanPadTokens
+// zero tokens past the last one, which covers the rows a tile of a document
+// shorter than 16 tokens reads past its end.
 constexpr int kWaveInfoWords = 8;
 constexpr int kScanMaxDocsPerWave = 63;
 constexpr int kScanWavesPerGroup = 4;
@@ -72,7 +77,8 @@ constexpr int kScanPrefetch = MSIM_SCAN_PREFETCH;  // ring depth: tiles in fligh
 #define MSIM_SCAN_WAVES_PER_CU 8
 #endif
 constexpr int kScanWavesPerCu = MSIM_SCAN_WAVES_PER_CU;  // scan waves launched per CU
-constexpr uint32_t kScanPastEnd = 0x3FFFFF0u;      // (kScanPastEnd + 15) * 64 + 48 < 2^32
+constexpr uint32_t kScanPadEntry = 0u;  // tile entry of a padding slot
+constexpr int64_t kScanPadTokens = 16;  // zero tokens past the end of every corpus buffer the scan reads
 struct ScanArgs {
   const uint8_t* codes;         // [num_tokens, 64] int4 nibbles
   const float* token_scale16;   // [num_tokens] token scales / 16 (kScanEpiFma), the token scales

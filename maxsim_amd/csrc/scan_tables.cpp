@@ -66,6 +66,10 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
     // LPT over the whole corpus: absolute token starts and document ids
     // (every wave's base is token 0, document 0).
     waves = std::min(waves, n);
+    // With more than one workgroup, the first one gets no documents: in a
+    // fused launch it selects the top-k, and its polling would otherwise
+    // slow its own scan work and that of the workgroup sharing its CU.
+    const int64_t first = waves > kScanWavesPerGroup ? kScanWavesPerGroup : 0;
     std::vector<int64_t> order;
     order.reserve((size_t)n);
     for (int64_t d = 0; d < n; ++d)
@@ -74,7 +78,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
                      [&](int64_t a, int64_t b) { return doc_cost(off, a) > doc_cost(off, b); });
     using Load = std::pair<int64_t, int64_t>;  // (cost so far, wave)
     std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
-    for (int64_t w = 0; w < waves; ++w) heap.push({0, w});
+    for (int64_t w = first; w < waves; ++w) heap.push({0, w});
     std::vector<std::vector<int64_t>> docs((size_t)waves), empty_docs((size_t)waves);
     for (int64_t d : order) {
       Load l = heap.top();
@@ -83,7 +87,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
       heap.push({l.first + doc_cost(off, d), l.second});
     }
     for (int64_t d = 0, w = 0; d < n; ++d)
-      if (off[d + 1] == off[d]) empty_docs[(size_t)(w++ % waves)].push_back(d);
+      if (off[d + 1] == off[d]) empty_docs[(size_t)(first + w++ % (waves - first))].push_back(d);
     for (int64_t w = 0; w < waves; ++w) {
       auto& ds = docs[(size_t)w];
       std::sort(ds.begin(), ds.end());  // ascending tokens within the wave
@@ -91,7 +95,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
       for (int64_t d : ds) emit_doc_tiles(off[d], off[d + 1], d, tiles);
       empties.insert(empties.end(), empty_docs[(size_t)w].begin(), empty_docs[(size_t)w].end());
       add_wave(0, (int64_t)ds.size(), 0, T, tab0, e0, (int64_t)(ds.size() + empty_docs[(size_t)w].size()));
-      for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
+      for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPadEntry);
     }
   } else {
     // Contiguous ranges balanced by cost, at most kScanMaxDocsPerWave
@@ -112,7 +116,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
           else emit_doc_tiles(off[d] - T0, off[d + 1] - T0, d - d0, tiles);
         }
         add_wave(d0, e - d0, T0, off[e], tab0, e0, e - d0);
-        for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
+        for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPadEntry);
         d0 = e;
       }
     }
@@ -121,7 +125,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   while ((info.size() / kWaveInfoWords) % kScanWavesPerGroup != 0) {
     const int64_t tab0 = (int64_t)tiles.size(), e0 = (int64_t)empties.size();
     add_wave(n, 0, T, T, tab0, e0, 0);
-    for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPastEnd);
+    for (int k = 0; k <= kScanPrefetch; ++k) tiles.push_back(kScanPadEntry);
   }
   // Every wave's entries at a fixed stride (a multiple of 8 entries, 64 B),
   // so a wave finds them from its index alone, without reading its row of
@@ -130,7 +134,7 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   int64_t longest = 0;
   for (int64_t w = 0; w < num_waves; ++w) longest = std::max<int64_t>(longest, info[w * kWaveInfoWords + 4]);
   stride = ((longest + kScanPrefetch + 1 + 7) / 8) * 8;
-  table.assign((size_t)(num_waves * stride), kScanPastEnd);
+  table.assign((size_t)(num_waves * stride), kScanPadEntry);
   // Positions in wave order: wave w's documents take [pos0, pos0 + all_docs).
   std::vector<int64_t> block_pos;
   int64_t pos = 0;

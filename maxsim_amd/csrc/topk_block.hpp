@@ -567,12 +567,18 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
       third[j] = in ? (uint32_t)(c >> 32) : 0u;
       stale |= (uint32_t)in & ((uint32_t)!key_current(a) | (uint32_t)!key_current(b) | (uint32_t)((uint32_t)c != tag));
     }
-    if (__ballot(stale != 0) == 0) break;
+    const uint64_t stale_lanes = __ballot(stale != 0);
+    if (stale_lanes == 0) break;
     if (expired()) {
       give_up();
       return;
     }
-    __builtin_amdgcn_s_sleep(1);
+    // Poll gently while many workgroups are still scanning (the polls take
+    // issue slots from the scan waves sharing this CU), then closely.
+    const int nstale = __popcll(stale_lanes);
+    if (nstale > 32) __builtin_amdgcn_s_sleep(32);
+    else if (nstale > 4) __builtin_amdgcn_s_sleep(8);
+    else __builtin_amdgcn_s_sleep(1);
   }
   uint32_t lmax = 0;
 #pragma unroll

@@ -51,7 +51,7 @@ int main() {
           if (last) doc_tiles_last[doc]++;
           if (last != (start + rows == off[doc + 1])) { printf("BAD last\n"); return 1; }
         }
-        for (int64_t i = r[4]; i < stride; ++i) if (table[w * stride + i] != msim::kScanPastEnd) { printf("BAD pad\n"); return 1; }
+        for (int64_t i = r[4]; i < stride; ++i) if (table[w * stride + i] != msim::kScanPadEntry) { printf("BAD pad\n"); return 1; }
         for (int64_t e = 0; e < r[6]; ++e) seen_empty[info[nw * 8 + r[7] + e]]++;
       }
       for (int d = 0; d < n; ++d) {
