@@ -435,17 +435,20 @@ __device__ void wave_topk(const float* __restrict__ row, int64_t n, int k,
 // and tag never decide).
 //
 // Selection: lane l holds the records of blocks l, l + 64, ...; T, the k-th
-// largest of the 64 lane maxima (ties counted; a radix selection by ballot
-// counts), is at most the row's k-th largest score key, because k lanes hold a
-// block maximum >= T, each a different document's key.  So every key of the
-// top-k is >= T and lies in a block whose maximum is >= T (a "hot" block).
-// A hot block whose third score key is below T has all its keys >= T in its
+// largest of the 64 lane maxima (ties counted; each lane counts the maxima at
+// least its own), is at most the row's k-th largest score key, because k
+// lanes hold a block maximum >= T, each a different document's key.  So
+// every key of the top-k is >= T and lies in a block whose maximum is >= T.
+// A block whose third score key is below T has all its keys >= T in its
 // record; a deeper one has its keys loaded (eight lanes per block, two keys
 // each, a second round trip).  The keys >= T are appended to a candidate
 // list in LDS and each one's rank counted against the whole list (broadcast
-// LDS reads).  More than kTailHotMax hot blocks, a deep one of more than
-// kTailBlockKeys documents, or cap = 0 fall back to k rounds of a wave
-// maximum over the whole row.
+// LDS reads).  More than kTailHotMax deep blocks, a deep one of more than
+// kTailBlockKeys documents, more candidates than the list holds, or cap = 0
+// fall back to k rounds of a wave maximum over the whole row.  Every step
+// after the last record's poll is a fixed sequence of independent
+// instructions: one wave selects, and a chain of dependent ones would cost
+// it several cycles each.
 constexpr int kTailBlocks = 512;                            // workgroups at most
 constexpr int kTailBlocksPerLane = kTailBlocks / kWave;     // 8
 constexpr int kTailHotMax = 48;                             // hot blocks of the fast path at most
@@ -453,10 +456,12 @@ constexpr int kTailBlockKeys = 16;                          // documents per dee
 constexpr int kTailMaxDocs = 4096;                          // ids below 2^12
 constexpr int kTailTagBits = 19;
 constexpr uint32_t kTailTagMask = (1u << kTailTagBits) - 1u;
-// LDS of the selecting wave: candidates (at most kTailBlockKeys per hot
-// block, then eight zero keys), then the list of deep blocks.
+// LDS of the selecting wave: candidates (at most kTailCandMax, then eight
+// zero keys, then a spare slot for the stores of lanes without a
+// candidate), then the list of deep blocks (kTailHotMax entries and a spare).
 constexpr int kTailCandMax = kTailHotMax * kTailBlockKeys;
-constexpr int kTailLdsBytes = (kTailCandMax + 8) * 8 + kWave * 4;
+constexpr int kTailSpare = kTailCandMax + 8;
+constexpr int kTailLdsBytes = (kTailCandMax + 9) * 8 + (kTailHotMax + 1) * 4;
 
 __device__ __forceinline__ uint32_t tail_key(uint32_t u) {
   const uint32_t s = (uint32_t)((int32_t)u >> 31);
@@ -527,7 +532,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   typedef __attribute__((address_space(3))) uint64_t lds_u64;
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
   lds_u64* cand = (lds_u64*)lds_arg;
-  lds_u32* deep_list = (lds_u32*)(cand + kTailCandMax + 8);
+  lds_u32* deep_list = (lds_u32*)(cand + kTailSpare + 1);
   const int lane = lane_id();
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(keys, (uint32_t)n * 8u);
   const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
@@ -583,51 +588,67 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   uint32_t lmax = 0;
 #pragma unroll
   for (int j = 0; j < kTailBlocksPerLane; ++j) lmax = max(lmax, (uint32_t)(w0[j] >> 32));
-  // T: the largest value that k lane maxima reach, bit by bit from the top
-  // (ballot counts); T >= 1, so blocks without documents (maximum 0) are
+  // T: the largest lane maximum that k lane maxima reach (ties counted).
+  // Each lane counts the lane maxima at least its own (broadcast reads of
+  // all 64 from LDS, independent compares); T is the largest maximum whose
+  // count reaches k.  T >= 1, so blocks without documents (maximum 0) are
   // never hot.
-  uint32_t t = 0;
+  lds_u32* lm = (lds_u32*)cand;
+  lm[lane] = lmax;
+  wave_sync_lds();
+  int ge0 = 0, ge1 = 0;
 #pragma unroll
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t c = t | (1u << bit);
-    t = __popcll(__ballot(lmax >= c)) >= k ? c : t;
+  for (int j = 0; j < kWave; j += 8) {
+    const v4u q0 = *(const __attribute__((address_space(3))) v4u*)(lm + j);
+    const v4u q1 = *(const __attribute__((address_space(3))) v4u*)(lm + j + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ge0 += q0[e] >= lmax ? 1 : 0;
+      ge1 += q1[e] >= lmax ? 1 : 0;
+    }
   }
-  t = max(t, 1u);
-  // Hot blocks (maximum >= T), deep ones (a third key >= T, so hot too; listed
-  // in LDS for the second round trip) and the record keys >= T of the others,
-  // counted by one scan: candidates in bits 20.., hot blocks in bits 10..19,
-  // deep ones in bits 0..9.
-  int nh = 0, nd = 0, nc = 0;
-  bool wide = false;
+  const uint32_t t = max(wave_reduce(ge0 + ge1 >= k ? lmax : 0u, [](uint32_t x, uint32_t y) { return max(x, y); }), 1u);
+  wave_sync_lds();
+  // Per lane: its deep blocks (a third key >= T: all their keys are loaded;
+  // bit j of dmask) and the record keys >= T of its other blocks (bits 2j,
+  // 2j + 1 of cmask).  One scan gives every lane its offsets; each lane then
+  // writes its 16 record keys and 8 block ranges unconditionally, those it
+  // does not hold to a spare slot (no branches: one wave runs this, and a
+  // branch costs it far more than a store).
+  uint32_t dmask = 0, cmask = 0, wide = 0;
 #pragma unroll
   for (int j = 0; j < kTailBlocksPerLane; ++j) {
-    const bool deep = third[j] >= t;
-    nh += (uint32_t)(w0[j] >> 32) >= t ? 1 : 0;
-    nd += deep ? 1 : 0;
-    nc += !deep && (uint32_t)(w0[j] >> 32) >= t ? 1 : 0;
-    nc += !deep && (uint32_t)(w1[j] >> 32) >= t ? 1 : 0;
-    wide = wide || (deep && len[j] > kTailBlockKeys);
+    const uint32_t d = third[j] >= t ? 1u : 0u;
+    dmask |= d << j;
+    wide |= d & (len[j] > kTailBlockKeys ? 1u : 0u);
+    cmask |= ((d ^ 1u) & ((uint32_t)(w0[j] >> 32) >= t ? 1u : 0u)) << (2 * j);
+    cmask |= ((d ^ 1u) & ((uint32_t)(w1[j] >> 32) >= t ? 1u : 0u)) << (2 * j + 1);
   }
-  const uint32_t incl = wave_inclusive_scan(((uint32_t)nc << 20) | ((uint32_t)nh << 10) | (uint32_t)nd);
+  const uint32_t lc = (uint32_t)__popc(cmask), ld = (uint32_t)__popc(dmask);
+  const uint32_t incl = wave_inclusive_scan((lc << 16) | ld);
   const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
-  const int ndeep = (int)(tot & 0x3FFu), nhot = (int)((tot >> 10) & 0x3FFu);
-  if (cap > 0 && nhot <= kTailHotMax && __ballot(wide) == 0) {
-    // Record keys >= T of the blocks that are not deep.
-    int ncand = (int)(tot >> 20);
-    {
-      int o = (int)(incl >> 20) - nc;
+  const int ndeep = (int)(tot & 0xFFFFu);
+  int ncand = (int)(tot >> 16);
+  const bool fast = cap > 0 && ndeep <= kTailHotMax && __ballot(wide != 0) == 0 &&
+                    ncand + kTailBlockKeys * ndeep <= kTailCandMax;
+  if (fast) {
+    const uint32_t cbase = (incl >> 16) - lc, dbase = (incl & 0xFFFFu) - ld;
 #pragma unroll
-      for (int j = 0; j < kTailBlocksPerLane; ++j) {
-        const bool shallow = third[j] < t;
-        if (shallow && (uint32_t)(w0[j] >> 32) >= t) cand[o++] = w0[j];
-        if (shallow && (uint32_t)(w1[j] >> 32) >= t) cand[o++] = w1[j];
-      }
+    for (int slot = 0; slot < 2 * kTailBlocksPerLane; ++slot) {
+      const uint64_t key = (slot & 1) ? w1[slot >> 1] : w0[slot >> 1];
+      const uint32_t at = cbase + (uint32_t)__popc(cmask & ((1u << slot) - 1u));
+      cand[((cmask >> slot) & 1u) ? at : (uint32_t)kTailSpare] = key;
     }
     if (ndeep > 0) {
-      int o = (int)(incl & 0x3FFu) - nd;
 #pragma unroll
-      for (int j = 0; j < kTailBlocksPerLane; ++j)
-        if (third[j] >= t) deep_list[o++] = ((uint32_t)bs[j] << 8) | (uint32_t)len[j];
+      for (int j = 0; j < kTailBlocksPerLane; ++j) {
+        const uint32_t at = dbase + (uint32_t)__popc(dmask & ((1u << j) - 1u));
+        deep_list[((dmask >> j) & 1u) ? at : (uint32_t)kTailHotMax] = ((uint32_t)bs[j] << 8) | (uint32_t)len[j];
+      }
+    }
+  }
+  if (fast) {
+    if (ndeep > 0) {
       wave_sync_lds();
       // Round trip 2: eight lanes per deep block, two keys each (past the
       // block's count: out of range, key 0), all rounds issued together,
