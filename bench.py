@@ -42,6 +42,17 @@ SCAN_KERNEL = "int8q_scan_kernel<8, 1, true, false>"  # the scan (one-fma epilog
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "int8q_scan_config2_traffic.md")
 CALIBRATION_BYTES = 256 << 20  # one plain copy: reads and writes this many bytes
 SCAN_BLOCK = 10  # scan launches between two events
+KERNEL_STATS = os.path.join(ROOT, "profiles", "int8q_scan_config2_kernel_stats.md")
+MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+# The achievable bound of the fused scan under its present design, from
+# measured constants: a tile's 16 MFMAs at the rate of an MFMA followed by
+# three VALU instructions with two waves per SIMD (a rate test with no memory
+# traffic: 11.6 ns per MFMA), plus the time until a wave's first tiles land
+# (median wave, per-wave s_memrealtime stamps: 1.4 us) and the tail from the
+# last wave's loop end to the end of the selection (stamps: 3.5 us).
+MIX_NS_PER_MFMA = 11.6
+RAMP_US = 1.4
+TAIL_US = 3.5
 
 
 def parse_args():
@@ -129,19 +140,61 @@ def read_traffic() -> float | None:
     return None
 
 
-def host_metadata() -> dict:
-    """What the run was: command, host CPU model and core counts, GPU, ROCm."""
-    model = None
+def read_kernel_stats_us(kernel: str) -> float | None:
+    """The committed rocprofv3 average duration (us) of `kernel`, from the
+    table of the config-2 kernel-stats summary, if any."""
     try:
-        with open("/proc/cpuinfo") as fh:
+        with open(KERNEL_STATS) as fh:
             for line in fh:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
+                cells = [c.strip().strip("`") for c in line.split("|")]
+                if len(cells) > 3 and cells[1] == kernel:
+                    return float(cells[3])
+    except (OSError, ValueError):
+        return None
+    return None
+
+
+def scan_tiles(offsets: np.ndarray) -> int:
+    """16-token tiles of the scan: ceil(len / 16) per non-empty document."""
+    lens = np.diff(offsets)
+    return int(((lens + 15) // 16).sum())
+
+
+def lscpu_fields() -> dict:
+    """The host CPU as `lscpu` names it (model name, BIOS model name, family,
+    model, stepping, sockets), or the /proc/cpuinfo model name without lscpu."""
+    import subprocess
+
+    keys = ("Vendor ID", "Model name", "BIOS Model name", "CPU family", "Model", "Stepping",
+            "Socket(s)", "Core(s) per socket", "Thread(s) per core")
+    out = {}
+    try:
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10,
+                              env=dict(os.environ, LC_ALL="C")).stdout
+        for line in text.splitlines():
+            name, _, value = line.partition(":")
+            if name.strip() in keys and name.strip() not in out:
+                out[name.strip()] = value.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
+    if "Model name" not in out:
+        try:
+            with open("/proc/cpuinfo") as fh:
+                for line in fh:
+                    if line.startswith("model name"):
+                        out["Model name"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    return out
+
+
+def host_metadata() -> dict:
+    """What the run was: command, host CPU (lscpu) and core counts, GPU, ROCm."""
+    cpu = lscpu_fields()
     meta = {"benchmark_command": " ".join([os.path.basename(sys.executable)] + sys.argv),
-            "cpu_model": model, "nproc": os.cpu_count(), "cpus_allowed": len(os.sched_getaffinity(0))}
+            "cpu_model": cpu.get("Model name"), "lscpu": cpu, "nproc": os.cpu_count(),
+            "cpus_allowed": len(os.sched_getaffinity(0))}
     try:
         import torch
 
@@ -320,6 +373,14 @@ def bench_config2(args):
     nbytes = algorithmic_bytes(num_tokens, num_docs, batch, qtok, k, -(-min(cus * 8, num_docs) // 4))
     scan_avg_s = float(scan_ms.mean()) * 1e-3
     achieved = nbytes["total"] / scan_avg_s / 1e9
+    # MFMA work of the scan: 2 * rows * tokens * 128 int8 operations.
+    mfma_ops = 2.0 * batch * qtok * num_tokens * 128
+    # The achievable bound: the tiles of one SIMD (two scanning waves; the
+    # first workgroup's waves scan nothing) at the mix rate, plus ramp and tail.
+    waves = 4 * (-(-min(cus * 8, num_docs) // 4))
+    tiles_per_simd = 2.0 * scan_tiles(packed.doc_offsets) / max(1, waves - 4)
+    bound_us = RAMP_US + tiles_per_simd * 16 * MIX_NS_PER_MFMA * 1e-3 + TAIL_US
+    rocprof_us = read_kernel_stats_us(SCAN_KERNEL)
 
 
     # ---- MALL-cold: rotate over corpus copies whose total exceeds the 256 MB cache.
@@ -436,15 +497,27 @@ def bench_config2(args):
             "scoring_only_frac": (nbytes["total"] - 4 * batch * num_docs - 12 * batch * k)
                                  / (float(score_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "dispatch_floor_ms": float(np.median(floor_ms)),
-            "frac_excluding_dispatch_floor": nbytes["total"]
-                                             / ((float(scan_ms.mean()) - float(np.median(floor_ms))) * 1e-3)
-                                             / 1e9 / HBM_PEAK_GBS,
+            "mfma_frac": mfma_ops / scan_avg_s / 1e12 / MFMA_INT8_PEAK_TOPS,
+            "mfma_ops_per_launch": mfma_ops,
+            "rocprof_kernel_us": rocprof_us,
+            "rocprof_frac": None if rocprof_us is None else nbytes["total"] / (rocprof_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "rocprof_source": "profiles/int8q_scan_config2_kernel_stats.md (rocprofv3 --kernel-trace --stats of "
+                              "this script, average duration of %s; committed, not measured in this run)" % SCAN_KERNEL,
+            "achievable_bound": {
+                "kernel_us": bound_us,
+                "frac": nbytes["total"] / (bound_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                "tiles_per_simd": tiles_per_simd,
+                "basis": "ramp %.1f us + tiles per SIMD x 16 MFMAs x %.1f ns (an MFMA and three VALU instructions, "
+                         "two waves per SIMD, rate test) + tail %.1f us (last loop end to selection end); "
+                         "ramp and tail from per-wave s_memrealtime stamps" % (RAMP_US, MIX_NS_PER_MFMA, TAIL_US),
+            },
             "cold_kernel_ms_avg": None if cold_scan_ms is None else float(cold_scan_ms.mean()),
             "cold_frac": None if cold_scan_ms is None
                          else nbytes["total"] / (float(cold_scan_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "traffic_source": "profiles/int8q_scan_config2_traffic.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE "
                               "runs of this script, calibrated by a plain copy)",
-            "note": "scan launches (with the fused top-10) back to back, averaged over blocks of %d; the "
+            "note": "frac, mfma_frac: scan launches (with the fused top-10) back to back between HIP events on "
+                    "the launch stream, averaged over blocks of %d (so each includes the launch-to-launch gap); the "
                     "35.7 MB corpus stays in the 256 MB MALL between launches (cold_*: each launch on the "
                     "next of %d corpus copies, %.0f MB in all)" % (SCAN_BLOCK, max(1, args.cold_copies),
                                                                   max(1, args.cold_copies) * nbytes["corpus"] / 1e6),
@@ -466,7 +539,6 @@ def bench_config2(args):
 # Secondary measurements (the driver's line is config 2).  Each returns the
 # same JSON fields, with `config.workload` naming the configuration.
 
-MFMA_INT8_PEAK_TOPS = 5000.0
 FP32_PEAK_TFLOPS = 157.3
 
 
