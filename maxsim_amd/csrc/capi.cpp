@@ -171,16 +171,20 @@ void upload_scaled(DeviceBuffer& dst, const float* src, int64_t count, float fac
   check_hip(hipMemcpy(dst.ptr, scaled.data(), scaled.size() * 4, hipMemcpyHostToDevice), what);
 }
 
-// int4 rows of row_bytes < 64 bytes widened to 64 bytes with zero nibbles
-// (zero codes add nothing to a dot product).
-void upload_codes128(DeviceBuffer& dst, const uint8_t* src, int64_t num_tokens, int64_t row_bytes,
-                     const char* what) {
-  if (row_bytes >= 64) {
+// int4 rows of row_bytes bytes (dim / 2) widened to the generalized
+// scorer's whole 128-dim chunks (64 bytes each) with zero nibbles, which add
+// nothing to a dot product; nothing is kept when the rows already are whole
+// chunks, or when dim is beyond what that scorer takes.
+void upload_codes_wide(DeviceBuffer& dst, const uint8_t* src, int64_t num_tokens, int64_t row_bytes,
+                       const char* what) {
+  const int chunks = score_chunks(2 * row_bytes);
+  const int64_t width = 64 * (int64_t)chunks;
+  if (chunks == 0 || row_bytes == width) {
     dst.reset();
     return;
   }
-  std::vector<uint8_t> wide((size_t)std::max<int64_t>(num_tokens, 1) * 64, 0);
-  for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 64], src + t * row_bytes, (size_t)row_bytes);
+  std::vector<uint8_t> wide((size_t)(std::max<int64_t>(num_tokens, 1) * width), 0);
+  for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * width], src + t * row_bytes, (size_t)row_bytes);
   dst.ensure(wide.size(), what);
   check_hip(hipMemcpy(dst.ptr, wide.data(), wide.size(), hipMemcpyHostToDevice), what);
 }
@@ -480,7 +484,7 @@ extern "C" int msim_int4_create(const uint8_t* packed, int64_t num_tokens, int64
       check_hip(hipMemcpy(h->packed.ptr, packed, h->packed_size, hipMemcpyHostToDevice), "copy int4 packed docs to device");
     check_hip(hipMemset(h->packed.as<uint8_t>() + h->packed_size, 0, pad_bytes), "zero int4 packed docs padding");
     check_hip(hipMemcpy(h->offsets.ptr, offsets, h->offsets_size * 8, hipMemcpyHostToDevice), "copy int4 offsets to device");
-    if (dim < 128) upload_codes128(h->codes128, packed, num_tokens, row_bytes, "int4 packed docs (128 dims)");
+    upload_codes_wide(h->codes_wide, packed, num_tokens, row_bytes, "int4 packed docs (whole 128-dim chunks)");
     // The int8-query scan's tables, built here so that the first search (and
     // msim_int4_topk_int8q_noalloc) finds them resident.
     if (dim == 128 && h->num_docs > 0) build_wave_info(h.get(), scan_waves(h.get()));
@@ -533,7 +537,7 @@ extern "C" int msim_int4_set_residual(msim_int4_docs* h, const uint8_t* packed, 
     const size_t pbytes = (size_t)num_tokens * (size_t)row_bytes;
     h->residual_packed.ensure(std::max<size_t>(pbytes, 64), "hipMalloc resident int4 residual data");
     if (pbytes) check_hip(hipMemcpy(h->residual_packed.ptr, packed, pbytes, hipMemcpyHostToDevice), "copy int4 residual data to device");
-    upload_codes128(h->residual128, packed, num_tokens, row_bytes, "int4 residual data");
+    upload_codes_wide(h->residual_wide, packed, num_tokens, row_bytes, "int4 residual data");
     upload_scaled(h->residual_token_scales16, token_scales, count, 0.0625f, "int4 residual token scales");
     h->residual_scale = scale;
     h->has_residual = true;

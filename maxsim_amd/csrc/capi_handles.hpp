@@ -32,7 +32,7 @@ struct ScoreWorkspace {
 
 // Which query the generalized path scores.
 struct QueryInput {
-  const float* d_query = nullptr;    // fp32 [rows, 128] (device or pinned host memory), or
+  const float* d_query = nullptr;    // fp32 [rows, 128 chunks] (device or pinned host memory), or
   const uint8_t* d_qbits = nullptr;  // sign bits [rows, 16] (pack_signs order)
   int limbs = 3;                     // 3: fp32 split into int8 limbs, 1: int8
   bool recip = false;                // int8 rounding q * (1 / sigma) (binary int8q)
@@ -54,6 +54,7 @@ struct DocStreams {
   const float* doc_scale = nullptr;
   float scale = 1.0f;
   bool unit_tscale = false;  // tscale is all ones
+  int chunks = 1;            // 128-dim chunks per token (score_chunks(dim))
 };
 
 // Candidate targets: none (every document), one list shared by all batch
@@ -77,7 +78,7 @@ struct CandidateLayout {
   int64_t waves = 0, per_wave = 0, cap = 0;
 };
 CandidateLayout candidate_layout(int64_t batch, int64_t query_tokens, int limbs, int64_t per_target,
-                                 int64_t max_doc_tiles);
+                                 int64_t max_doc_tiles, int chunks = 1);
 
 // Scores of `batch` x `query_tokens` query rows against the targets into
 // d_out[b * out_stride + t] (and d_iout[b * targets + t] as int32 if set).
@@ -110,9 +111,10 @@ struct msim_int4_docs {
   int64_t block_pos_off = 0;      // index of the workgroup start positions in wave_info
   msim::DeviceBuffer wave_info, tile_table;
   msim::DeviceBuffer packed, offsets, token_scales, token_scales16, residual_packed, residual_token_scales16;
-  // Generalized path: codes padded to 64 bytes per token when dim < 128,
-  // per-token 1/16 when the corpus has no token scales.
-  msim::DeviceBuffer codes128, residual128, ones16;
+  // Generalized path: codes widened to whole 128-dim chunks (64 bytes each)
+  // when dim is not a multiple of 128, per-token 1/16 when the corpus has no
+  // token scales.
+  msim::DeviceBuffer codes_wide, residual_wide, ones16;
   // workspaces (grow monotonically, freed with the handle; cu:3057-3067)
   msim::DeviceBuffer qpack, qscale, qbias, scores, rowmax;
   msim::HostBuffer host_io;  // synchronous calls: query in, results out (pinned)
@@ -123,7 +125,7 @@ struct msim_int4_docs {
 
   uint64_t resident_bytes() const {
     return packed_size + offsets_size * 8 + token_scales.cap + token_scales16.cap + residual_packed.cap +
-           residual_token_scales16.cap + codes128.cap + residual128.cap + ones16.cap;
+           residual_token_scales16.cap + codes_wide.cap + residual_wide.cap + ones16.cap;
   }
   uint64_t workspace_bytes() const {
     return qpack.cap + qscale.cap + qbias.cap + scores.cap +
@@ -140,7 +142,7 @@ struct msim_binary_docs {
   bool has_scale_vector = false;
   bool has_token_scale = false;
   std::vector<int64_t> host_offsets;
-  // codes padded to 16 bytes (128 dims) per token
+  // codes padded to whole 128-dim chunks (16 bytes each) per token
   msim::DeviceBuffer packed, offsets, scale_vector, token_scales, ones, scale_override;
   // int4 residual stream of the binary-prefix + int4-residual format
   bool has_residual = false;

@@ -42,8 +42,8 @@ T* upload_vec(DeviceBuffer& buf, const std::vector<T>& v, const char* what, hipS
 }  // namespace
 
 CandidateLayout candidate_layout(int64_t batch, int64_t query_tokens, int limbs, int64_t per_target,
-                                 int64_t max_doc_tiles) {
-  const int64_t rpp = score_rows_per_pass(limbs, query_tokens);
+                                 int64_t max_doc_tiles, int chunks) {
+  const int64_t rpp = score_rows_per_pass(limbs, query_tokens, chunks);
   const int64_t subs = ceil_div(query_tokens, rpp);
   int64_t waves = ceil_div((int64_t)device_cu_count() * 8, batch * subs);
   waves = std::max<int64_t>(1, std::min(waves, per_target));
@@ -72,9 +72,12 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   }
   const int limbs = q.limbs;
   const int64_t rows_padded = ceil_div(rows, 16) * 16 + 128;
+  const int chunks = s.chunks;
+  if (chunks != 1 && (limbs != 3 || q.d_qbits || q.alt_int4 || q.from_alt || (s.doc == kDocSign && s.residual)))
+    throw NotSupported("dims above 128 are scored for fp32 queries against int4 or sign documents only");
 
   // 1. Quantise the query rows.
-  ws.qpack.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs");
+  ws.qpack.ensure((size_t)limbs * rows_padded * 128 * chunks, "hipMalloc query limbs");
   ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
   ws.qsum.ensure(sizeof(int32_t) * limbs * rows_padded, "hipMalloc query limb sums");
   if (q.alt_int4) ws.qpack_alt.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs (int4 layout)");
@@ -89,7 +92,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
     // lane order, so both share the int4 query layout.
     check_hip(launch_quantize_limbs(q.d_query, rows, rows_padded, limbs, s.residual ? kDocInt4 : s.doc, q.recip,
                                     ws.qpack.as<int8_t>(), ws.colmul.as<float>(), ws.qsum.as<int32_t>(), stream,
-                                    kDocInt4, q.alt_int4 ? ws.qpack_alt.as<int8_t>() : nullptr),
+                                    kDocInt4, q.alt_int4 ? ws.qpack_alt.as<int8_t>() : nullptr, chunks),
               "launch query quantize kernel");
 
   // 2. Reducer weights, one per query row (padding rows 0).
@@ -109,7 +112,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   // 3. Work split.
   const int64_t groups = t.per_row ? batch : 1;
   const int64_t grp_rows = t.per_row ? query_tokens : rows;
-  const int64_t rpp = score_rows_per_pass(limbs, grp_rows);
+  const int64_t rpp = score_rows_per_pass(limbs, grp_rows, chunks);
   const int64_t subs = ceil_div(grp_rows, rpp);
   const int64_t per_target = t.per_row ? t.count : targets;
   int64_t waves = ceil_div((int64_t)device_cu_count() * 8, groups * subs);
@@ -122,7 +125,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
     // more than one per wave, tables written by candidate_tables_kernel (or
     // already by the selector).
     if (!t.per_row) throw InvalidArgument("device candidate lists must be per batch row");
-    const CandidateLayout cl = candidate_layout(batch, query_tokens, limbs, per_target, t.max_doc_tiles);
+    const CandidateLayout cl = candidate_layout(batch, query_tokens, limbs, per_target, t.max_doc_tiles, chunks);
     const int64_t w4 = cl.waves;
     d_targets = t.device;
     if (cl.per_wave == 1) {
@@ -209,6 +212,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   a.temperature = temperature;
   a.unit_tscale = s.unit_tscale;
   a.query_tokens = (int32_t)query_tokens;
+  a.chunks = chunks;
   // Passes that hold whole batch rows let the kernel sum them itself.
   const bool in_kernel_sum = t.per_row ? subs == 1 : rpp % query_tokens == 0;
   if (in_kernel_sum) {
@@ -287,21 +291,22 @@ void check_k(int64_t k, int64_t n) {
   if (k > kTopkMaxK) throw NotSupported("k above 4096 is not supported by the device top-k selector");
 }
 
-// fp32 query [B, Q, dim] (host) -> device [B * Q, 128], zero-padded dims.
-// The fp32 query of a synchronous call as [rows, 128] (zero-padded from dim)
-// in the workspace's pinned host buffer: the quantisation kernels read it
-// there, so no staging copy is queued.
-const float* stage_query128(ScoreWorkspace& ws, const float* query, int64_t rows, int64_t dim) {
-  const size_t bytes = sizeof(float) * (size_t)std::max<int64_t>(rows, 1) * 128;
+// The fp32 query [B, Q, dim] of a synchronous call as [rows, 128 chunks]
+// (zero-padded from dim to whole 128-dim chunks) in the workspace's pinned
+// host buffer: the quantisation kernels read it there, so no staging copy is
+// queued.
+const float* stage_query(ScoreWorkspace& ws, const float* query, int64_t rows, int64_t dim) {
+  const int64_t width = 128 * (int64_t)std::max(1, score_chunks(dim));
+  const size_t bytes = sizeof(float) * (size_t)(std::max<int64_t>(rows, 1) * width);
   ws.host_query.ensure(bytes, "hipHostMalloc query staging");
   float* q = ws.host_query.as<float>();
   if (rows == 0) return q;
-  if (dim == 128) {
-    std::memcpy(q, query, sizeof(float) * (size_t)rows * 128);
+  if (dim == width) {
+    std::memcpy(q, query, sizeof(float) * (size_t)(rows * width));
   } else {
     for (int64_t r = 0; r < rows; ++r) {
-      std::memcpy(q + r * 128, query + r * dim, sizeof(float) * (size_t)dim);
-      std::memset(q + r * 128 + dim, 0, sizeof(float) * (size_t)(128 - dim));
+      std::memcpy(q + r * width, query + r * dim, sizeof(float) * (size_t)dim);
+      std::memset(q + r * width + dim, 0, sizeof(float) * (size_t)(width - dim));
     }
   }
   return q;
@@ -340,7 +345,7 @@ void copy_scores_out(ScoreWorkspace& ws, void* out, const void* d, size_t bytes)
 // ------------------------------------------------------------------ int4
 
 DocStreams int4_streams(msim_int4_docs* h, bool residual) {
-  if (h->dim > 128) throw NotSupported("fp32-query int4 scoring currently supports dim <= 128");
+  if (h->dim > kScoreMaxDim) throw NotSupported("fp32-query int4 scoring currently supports dim <= 512");
   if (h->num_tokens > 0 && !h->has_token_scale && h->ones16.cap < (size_t)h->num_tokens * 4) {
     std::vector<float> ones((size_t)h->num_tokens, 0.0625f);
     h->ones16.ensure(ones.size() * 4, "hipMalloc int4 unit token scales");
@@ -348,7 +353,8 @@ DocStreams int4_streams(msim_int4_docs* h, bool residual) {
   }
   DocStreams s;
   s.doc = kDocInt4;
-  s.codes = h->dim < 128 ? h->codes128.as<uint8_t>() : h->packed.as<uint8_t>();
+  s.chunks = score_chunks(h->dim);
+  s.codes = h->codes_wide.ptr ? h->codes_wide.as<uint8_t>() : h->packed.as<uint8_t>();
   s.tscale = h->has_token_scale ? h->token_scales16.as<float>() : h->ones16.as<float>();
   s.tmul = (float)h->scale;
   s.scale = 1.0f;
@@ -356,7 +362,7 @@ DocStreams int4_streams(msim_int4_docs* h, bool residual) {
     if (!h->has_residual)
       throw InvalidArgument("residual int4 data was requested but is not loaded on this CUDA handle");
     s.residual = true;
-    s.rcodes = h->dim < 128 ? h->residual128.as<uint8_t>() : h->residual_packed.as<uint8_t>();
+    s.rcodes = h->residual_wide.ptr ? h->residual_wide.as<uint8_t>() : h->residual_packed.as<uint8_t>();
     s.rtscale = h->residual_token_scales16.as<float>();
     s.rmul = (float)h->residual_scale;
   }
@@ -374,7 +380,7 @@ float* int4_score_device(msim_int4_docs* h, const float* query, int64_t batch, i
                          int64_t m, bool residual, hipStream_t stream) {
   const int64_t targets = cand ? m : h->num_docs;
   const DocStreams s = int4_streams(h, residual);
-  const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+  const float* d_query = stage_query(h->ws, query, batch * query_tokens, dim);
   h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
   QueryInput qi;
   qi.d_query = d_query;
@@ -464,6 +470,7 @@ DocStreams binary_streams(msim_binary_docs* h, double scale, bool use_scale_vect
   s.doc_scale = d_scale_override ? d_scale_override : (use_scale_vector ? h->scale_vector.as<float>() : nullptr);
   s.scale = (float)scale;
   s.unit_tscale = !use_token_scale;
+  s.chunks = score_chunks(h->dim);
   return s;
 }
 
@@ -471,7 +478,7 @@ float* binary_score_device(msim_binary_docs* h, const float* query, int64_t batc
                            int64_t dim, int limbs, bool recip, const DocStreams& s, int reducer,
                            const std::vector<float>& w, float temperature, const int64_t* cand, int64_t m) {
   const int64_t targets = cand ? m : h->num_docs;
-  const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+  const float* d_query = stage_query(h->ws, query, batch * query_tokens, dim);
   h->scores.ensure(sizeof(float) * std::max<int64_t>(1, batch * targets), "hipMalloc score cache");
   QueryInput qi;
   qi.d_query = d_query;
@@ -509,7 +516,7 @@ extern "C" int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int
     *out = nullptr;
     if (dim <= 0 || dim % 8 != 0) throw InvalidArgument("dim must be positive and divisible by 8");
     if (row_bytes != dim / 8) throw InvalidArgument("packed shape does not match dim");
-    if (dim > 128) throw NotSupported("binary scoring currently supports dim <= 128");
+    if (dim > kScoreMaxDim) throw NotSupported("binary scoring currently supports dim <= 512");
     if (num_tokens < 0) throw InvalidArgument("packed must have shape [num_doc_tokens, dim / 8]");
     validate_offsets(offsets, num_offsets, num_tokens);
     if (num_tokens > 0 && packed == nullptr) throw InvalidArgument("packed must not be NULL");
@@ -522,11 +529,12 @@ extern "C" int msim_binary_create(const uint8_t* packed, int64_t num_tokens, int
     h->host_offsets.assign(offsets, offsets + num_offsets);
     for (int64_t d = 0; d + 1 < num_offsets; ++d)
       h->max_doc_tiles = std::max<int64_t>(h->max_doc_tiles, (offsets[d + 1] - offsets[d] + 15) / 16);
-    // Rows widened to 16 bytes: padding bits meet zero query dims.  The
-    // int8-query scan of the sign stream may read kScanPadTokens rows past
-    // the end: zero rows follow.
-    std::vector<uint8_t> wide((size_t)(num_tokens + kScanPadTokens) * 16, 0);
-    for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * 16], packed + t * row_bytes, (size_t)row_bytes);
+    // Rows widened to whole 128-dim chunks (16 bytes each): padding bits meet
+    // zero query dims.  The int8-query scan of the sign stream (dim 128) may
+    // read kScanPadTokens rows past the end: zero rows follow.
+    const int64_t width = 16 * (int64_t)score_chunks(dim);
+    std::vector<uint8_t> wide((size_t)((num_tokens + kScanPadTokens) * width), 0);
+    for (int64_t t = 0; t < num_tokens; ++t) std::memcpy(&wide[t * width], packed + t * row_bytes, (size_t)row_bytes);
     upload_vec(h->packed, wide, "copy binary packed docs to device");
     std::vector<int64_t> offs(offsets, offsets + num_offsets);
     upload_vec(h->offsets, offs, "copy binary offsets to device");
@@ -839,7 +847,7 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
     select_device(h->device);
     const DocStreams prefix = int4_streams(h, false), fused = int4_streams(h, true);
     QueryInput qi;
-    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    qi.d_query = stage_query(h->ws, query, batch * query_tokens, dim);
     qi.limbs = 3;
     const float* wp = w.empty() ? nullptr : w.data();
     const HostTopk out(h->ws, batch, k);
@@ -871,7 +879,8 @@ extern "C" int msim_int4_cascade_topk(msim_int4_docs* h, const float* query, int
             run_generic_score(h->ws, h->host_offsets, h->num_tokens, fused, again, red, (float)temperature, batch,
                               query_tokens, wp, t, d, candidates, nullptr, nullptr);
           },
-          out.s, out.i, nullptr, candidate_layout(batch, query_tokens, qi.limbs, candidates, h->max_doc_tiles),
+          out.s, out.i, nullptr,
+          candidate_layout(batch, query_tokens, qi.limbs, candidates, h->max_doc_tiles, fused.chunks),
           h->offsets.as<int64_t>());
     }
     out.finish(out_scores, out_indices, nullptr);
@@ -1075,7 +1084,7 @@ extern "C" int msim_binary_binres_score(msim_binary_docs* h, const float* query,
     if (batch == 0 || targets == 0) return;
     select_device(h->device);
     QueryInput qi;
-    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    qi.d_query = stage_query(h->ws, query, batch * query_tokens, dim);
     qi.limbs = fused ? h->rescore_limbs : 1;
     Targets t{candidates, num_candidates, candidates != nullptr};
     h->scores.ensure(sizeof(float) * batch * targets, "hipMalloc score cache");
@@ -1099,7 +1108,7 @@ extern "C" int msim_binary_binres_topk(msim_binary_docs* h, const float* query, 
     if (batch == 0) return;
     select_device(h->device);
     QueryInput qi;
-    qi.d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    qi.d_query = stage_query(h->ws, query, batch * query_tokens, dim);
     qi.limbs = h->rescore_limbs;
     h->scores.ensure(sizeof(float) * batch * h->num_docs, "hipMalloc score cache");
     run_generic_score(h->ws, h->host_offsets, h->num_tokens, s, qi, kRedMax, 1.0f, batch, query_tokens, nullptr,
@@ -1121,7 +1130,7 @@ extern "C" int msim_binary_cascade_topk(msim_binary_docs* h, const float* query,
     binres_streams(h, true);
     if (batch == 0) return;
     select_device(h->device);
-    const float* d_query = stage_query128(h->ws, query, batch * query_tokens, dim);
+    const float* d_query = stage_query(h->ws, query, batch * query_tokens, dim);
     const HostTopk out(h->ws, batch, k);
     binres_cascade(h, d_query, batch, query_tokens, k, candidates, out.s, out.i, nullptr);
     out.finish(out_scores, out_indices, nullptr);

@@ -181,10 +181,10 @@ constexpr int kScoreInfoWords = 4;
 enum : int { kDocInt4 = 0, kDocSign = 1 };
 enum : int { kRedMax = 0, kRedTop2 = 1, kRedTop4 = 2, kRedLse = 3 };
 struct ScoreArgs {
-  const uint8_t* codes;        // int4 [T, 64] or sign bits [T, 16]
+  const uint8_t* codes;        // int4 [T, 64 chunks] or sign bits [T, 16 chunks]
   const float* tscale;         // [T] per-token scale of `codes` (never null)
   float tmul;                  // constant factor of the `codes` similarity
-  const uint8_t* rcodes;       // residual int4 codes [T, 64] (residual kernels)
+  const uint8_t* rcodes;       // residual int4 codes [T, 64 chunks] (residual kernels)
   const float* rtscale;        // [T] residual per-token scale
   float rmul;
   const int64_t* wave_info;    // [groups][num_waves][kScoreInfoWords]
@@ -198,7 +198,7 @@ struct ScoreArgs {
   int64_t info_grp_stride;     // int64 words between groups' wave tables (0 = shared)
   const int64_t* targets;      // document of each target, or nullptr (target = document)
   int64_t targets_grp_stride;  // entries between groups' target lists
-  const int8_t* qpack;         // [limbs][rows_padded][128] B-operand order
+  const int8_t* qpack;         // [limbs][rows_padded][128 chunks] B-operand order per 128-dim chunk
   int64_t rows_padded;
   const float* colmul;         // [rows_padded] per query row factor (sigma)
   const int32_t* qsum;         // [limbs][rows_padded] limb sums (sign documents)
@@ -220,13 +220,21 @@ struct ScoreArgs {
   int64_t iout_stride;
   int32_t query_tokens;
   bool unit_tscale;            // tscale is all ones (sign documents): integer maximum
+  int32_t chunks;              // 128-dim chunks per token and query row (1, 2 or 4)
 };
-int score_rows_per_pass(int limbs, int64_t rows);
+// Dims above 128 are scored in 128-dim chunks whose MFMA dots accumulate in
+// one int32 accumulator: 2 chunks up to 256 dims, 4 up to 512 (0: above).
+// 512 is the limit of the three-limb combination 254 a1 + a2 in int32
+// (|a| <= 128 * 127 * 512 < 2^23).
+constexpr int64_t kScoreMaxDim = 512;
+inline int score_chunks(int64_t dim) { return dim <= 128 ? 1 : dim <= 256 ? 2 : dim <= 512 ? 4 : 0; }
+int score_rows_per_pass(int limbs, int64_t rows, int chunks = 1);
 hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
                         hipStream_t stream);
+// Query rows of 128 * chunks floats (dims past the query's own zero).
 hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
                                  bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream,
-                                 int layout2 = 0, int8_t* qpack2 = nullptr);
+                                 int layout2 = 0, int8_t* qpack2 = nullptr, int chunks = 1);
 hipError_t launch_quantize_bits(const uint8_t* d_qbits, int64_t rows, int64_t rows_padded, int8_t* qpack,
                                 float* colmul, int32_t* qsum, hipStream_t stream);
 hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tokens, int64_t targets, int64_t bs,

@@ -142,33 +142,33 @@ struct ReducerState<kRedLse> {
 };
 
 // One tile of a stream, as loaded: lane (g, c) holds token c's bytes of lane
-// group g and the scales of token rows 4g .. 4g + 3.
-template <int DOC>
+// group g in each 128-dim chunk and the scales of token rows 4g .. 4g + 3.
+template <int DOC, int KC>
 struct TileCodes;
-template <>
-struct TileCodes<kDocInt4> {
-  v4u w;  // 16 bytes: dims 32g .. 32g + 31 as nibbles
+template <int KC>
+struct TileCodes<kDocInt4, KC> {
+  v4u w[KC];  // 16 bytes per chunk: dims 128 kc + 32g .. + 31 as nibbles
 };
-template <>
-struct TileCodes<kDocSign> {
-  unsigned w;  // 32 sign bits: dims 32g .. 32g + 31
+template <int KC>
+struct TileCodes<kDocSign, KC> {
+  unsigned w[KC];  // 32 sign bits per chunk: dims 128 kc + 32g .. + 31
 };
 
-// A operands (two MFMAs of 64 dims) from the tile bytes.
-__device__ __forceinline__ void unpack_a(const TileCodes<kDocInt4>& t, v4i& a0, v4i& a1) {
+// A operands (two MFMAs of 64 dims) from the tile bytes of one chunk.
+__device__ __forceinline__ void unpack_a(const v4u& w, v4i& a0, v4i& a1) {
   // Nibbles moved to the high half of each byte: the int8 value is 16 v.
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
-    a0[x] = (int)((t.w[x] << 4) & 0xF0F0F0F0u);  // even dims
-    a1[x] = (int)(t.w[x] & 0xF0F0F0F0u);         // odd dims
+    a0[x] = (int)((w[x] << 4) & 0xF0F0F0F0u);  // even dims
+    a1[x] = (int)(w[x] & 0xF0F0F0F0u);         // odd dims
   }
 }
-__device__ __forceinline__ void unpack_a(const TileCodes<kDocSign>& t, v4i& a0, v4i& a1) {
+__device__ __forceinline__ void unpack_a(unsigned w, v4i& a0, v4i& a1) {
   // Dword i holds bits i, i + 8, i + 16, i + 24 as bytes 0/1 (dims 32g + 8j + i).
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    a0[i] = (int)((t.w >> i) & 0x01010101u);
-    a1[i] = (int)((t.w >> (i + 4)) & 0x01010101u);
+    a0[i] = (int)((w >> i) & 0x01010101u);
+    a1[i] = (int)((w >> (i + 4)) & 0x01010101u);
   }
 }
 // Sign bits in the int4 lane order (a0: even dims, a1: odd dims), for a sign
@@ -176,10 +176,10 @@ __device__ __forceinline__ void unpack_a(const TileCodes<kDocSign>& t, v4i& a0, 
 // of a byte move to bits 0, 8, 16, 24 by one multiply with 0x41041 (shifts
 // 0, 6, 12, 18): the partial products overlap only at bits 6, 12 and 18,
 // whose carries stop at bits 7, 13 and 19, away from the kept bits.
-__device__ __forceinline__ void unpack_a_int4_order(const TileCodes<kDocSign>& t, v4i& a0, v4i& a1) {
+__device__ __forceinline__ void unpack_a_int4_order(unsigned w, v4i& a0, v4i& a1) {
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
-    const unsigned b = t.w >> (8 * x);
+    const unsigned b = w >> (8 * x);
     a0[x] = (int)(((b & 0x55u) * 0x41041u) & 0x01010101u);
     a1[x] = (int)((((b >> 1) & 0x55u) * 0x41041u) & 0x01010101u);
   }
@@ -188,10 +188,15 @@ __device__ __forceinline__ void unpack_a_int4_order(const TileCodes<kDocSign>& t
 // INTMAX (sign documents, one int8 limb, no token scale, MaxSim): the
 // +-1 dot 2 (q8 . bits) - sum(q8) is increasing in the MFMA result, so the
 // running maximum is kept on the int32 accumulators and converted once per
-// document.
-template <int DOC, bool RES, int L, int NT, int RED, bool INTMAX>
+// document.  KC: 128-dim chunks per token (dims above 128), each two more
+// MFMAs into the same accumulators.
+template <int DOC, bool RES, int L, int NT, int RED, bool INTMAX, int KC = 1>
 __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreArgs p) {
   static_assert(!INTMAX || (DOC == kDocSign && !RES && L == 1 && RED == kRedMax), "integer maximum form");
+  static_assert(KC == 1 || (L == 3 && !(DOC == kDocSign && RES)), "chunked dims: fp32 queries, one document format");
+  constexpr int kCodeBytes = (DOC == kDocInt4 ? 64 : 16) * KC;  // bytes per token of `codes`
+  constexpr int kResBytes = 64 * KC;                            // and of `rcodes`
+  constexpr int kQueryBytes = 128 * KC;                          // bytes per query row of a limb
   __shared__ float s_pool[kWavesPerGroup][16 * NT];
   const int lane = lane_id();
   const int wave = wave_uniform(threadIdx.x / kWave);
@@ -233,7 +238,7 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   const int64_t grow0 = (int64_t)grp * p.grp_rows + lr0;  // its global query row
 
   // Query B operands and per-column constants.
-  v4i bq[L][NT][2];
+  v4i bq[L][NT][KC][2];
   float colmul[NT], weight[NT];
   int qsum[L][NT];
 #pragma unroll
@@ -241,9 +246,12 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     const int64_t r = grow0 + 16 * j + c;
 #pragma unroll
     for (int l = 0; l < L; ++l) {
-      const v4i* src = reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + r) * 128 + 32 * g);
-      bq[l][j][0] = src[0];
-      bq[l][j][1] = src[1];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const v4i* src = reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + r) * kQueryBytes + 128 * kc + 32 * g);
+        bq[l][j][kc][0] = src[0];
+        bq[l][j][kc][1] = src[1];
+      }
       qsum[l][j] = DOC == kDocSign ? p.qsum[l * p.rows_padded + r] : 0;
     }
     colmul[j] = p.colmul[r];
@@ -261,8 +269,8 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
 
   struct Tile {
     uint64_t e;  // its table entry (table mode)
-    TileCodes<DOC> a;
-    TileCodes<kDocInt4> r;
+    TileCodes<DOC, KC> a;
+    TileCodes<kDocInt4, KC> r;
     float s[4], sr[4];
   };
   // Every load is unconditional: rows past a short document read its last
@@ -272,11 +280,14 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     const int64_t start = (int64_t)(e & kTileStartMask);
     const int rows1 = (int)((e >> kTileRowsShift) & 15);
     const int64_t tok = start + min(c, rows1);
-    if constexpr (DOC == kDocInt4)
-      t.a.w = *reinterpret_cast<const v4u*>(p.codes + tok * 64 + 16 * g);
-    else
-      t.a.w = *reinterpret_cast<const unsigned*>(p.codes + tok * 16 + 4 * g);
-    if constexpr (RES) t.r.w = *reinterpret_cast<const v4u*>(p.rcodes + tok * 64 + 16 * g);
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      if constexpr (DOC == kDocInt4)
+        t.a.w[kc] = *reinterpret_cast<const v4u*>(p.codes + tok * kCodeBytes + 64 * kc + 16 * g);
+      else
+        t.a.w[kc] = *reinterpret_cast<const unsigned*>(p.codes + tok * kCodeBytes + 16 * kc + 4 * g);
+      if constexpr (RES) t.r.w[kc] = *reinterpret_cast<const v4u*>(p.rcodes + tok * kResBytes + 64 * kc + 16 * g);
+    }
     if constexpr (!INTMAX) {
       // Token rows 4g .. 4g + 3 in one load; rows past the tile read 0
       // (buffer bounds at the tile's last row; they are masked below).
@@ -319,13 +330,14 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   struct Ops {
     v4i a0, a1, r0, r1;
   };
+  // (The pipelined form, one limb, always has one chunk.)
   auto unpack = [&](const Tile& t) {
     Ops o;
     if constexpr (DOC == kDocSign && RES)
-      unpack_a_int4_order(t.a, o.a0, o.a1);
+      unpack_a_int4_order(t.a.w[0], o.a0, o.a1);
     else
-      unpack_a(t.a, o.a0, o.a1);
-    if constexpr (RES) unpack_a(t.r, o.r0, o.r1);
+      unpack_a(t.a.w[0], o.a0, o.a1);
+    if constexpr (RES) unpack_a(t.r.w[0], o.r0, o.r1);
     return o;
   };
   // MFMAs of K half h of row block j (h = 0 starts from zero).
@@ -333,11 +345,11 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     const v4i zero = {0, 0, 0, 0};
 #pragma unroll
     for (int l = 0; l < L; ++l)
-      A.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][j][h], h ? A.s[l][j] : zero, 0, 0, 0);
+      A.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][j][0][h], h ? A.s[l][j] : zero, 0, 0, 0);
     if constexpr (RES) {
 #pragma unroll
       for (int l = 0; l < L; ++l)
-        A.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.r1 : o.r0, bq[l][j][h], h ? A.r[l][j] : zero, 0, 0, 0);
+        A.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.r1 : o.r0, bq[l][j][0][h], h ? A.r[l][j] : zero, 0, 0, 0);
     }
   };
   // Start of a tile's epilogue: its row count, and the document constants
@@ -373,8 +385,8 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
         // Limb dots combined smallest first; sign documents recover the
         // +-1 dot as 2 (q . bits) - sum(q).
         // int4 documents with three limbs: the two small limbs first as one
-        // exact integer, 254 a1 + a2 (|a| <= 16 * 7 * 127 * 128 < 2^21, so a
-        // 24-bit multiply is exact).
+        // exact integer, 254 a1 + a2 (|a| <= 128 * 127 * 128 KC < 2^23 for
+        // KC <= 4, so the 24-bit multiply and the int32 sum are exact).
         auto limbs3 = [&](const v4i (&a)[L][NT]) {
           const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
           return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
@@ -486,34 +498,46 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // All MFMAs of a tile: the first stream's halves, then the residual's
-  // (its operands unpacked only then, so fewer registers are live).
+  // All MFMAs of a tile: the first stream's halves, chunk by chunk, then the
+  // residual's (its operands unpacked only then, so fewer registers are
+  // live).  Chunk 0's first half starts from zero; every later MFMA adds to
+  // the same accumulators.
   auto issue = [&](Acc& Q, const Tile& tq) __attribute__((always_inline)) {
     const v4i zero = {0, 0, 0, 0};
-    v4i a0, a1;
-    if constexpr (DOC == kDocSign && RES)
-      unpack_a_int4_order(tq.a, a0, a1);
-    else
-      unpack_a(tq.a, a0, a1);
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int kc = 0; kc < KC; ++kc) {
+      v4i a0, a1;
+      if constexpr (DOC == kDocSign && RES)
+        unpack_a_int4_order(tq.a.w[kc], a0, a1);
+      else
+        unpack_a(tq.a.w[kc], a0, a1);
 #pragma unroll
-      for (int l = 0; l < L; ++l) Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][0], zero, 0, 0, 0);
+      for (int j = 0; j < NT; ++j)
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+        for (int l = 0; l < L; ++l)
+          Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][kc][0], kc == 0 ? zero : Q.s[l][j], 0, 0, 0);
 #pragma unroll
-      for (int l = 0; l < L; ++l) Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][1], Q.s[l][j], 0, 0, 0);
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+          Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[l][j][kc][1], Q.s[l][j], 0, 0, 0);
+    }
     if constexpr (RES) {
-      v4i r0, r1;
-      unpack_a(tq.r, r0, r1);
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+      for (int kc = 0; kc < KC; ++kc) {
+        v4i r0, r1;
+        unpack_a(tq.r.w[kc], r0, r1);
 #pragma unroll
-        for (int l = 0; l < L; ++l) Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][0], zero, 0, 0, 0);
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+          for (int l = 0; l < L; ++l)
+            Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][kc][0], kc == 0 ? zero : Q.r[l][j], 0, 0, 0);
 #pragma unroll
-        for (int l = 0; l < L; ++l) Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][1], Q.r[l][j], 0, 0, 0);
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int l = 0; l < L; ++l)
+            Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r1, bq[l][j][kc][1], Q.r[l][j], 0, 0, 0);
+      }
     }
   };
 
@@ -522,8 +546,9 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
   // the two-tile passes (candidate rescoring: few waves per SIMD, short
   // documents), one for eight row blocks (registers).  One-limb two-tile
   // passes interleave each tile's epilogue with the next tile's MFMAs (two
-  // accumulator sets); the others fence each tile.
-  constexpr int kAhead = NT <= 2 ? 3 : 1;
+  // accumulator sets); the others fence each tile.  Chunked dims hold more
+  // bytes per tile: one in flight.
+  constexpr int kAhead = NT <= 2 && KC == 1 ? 3 : 1;
   constexpr bool kPipe = NT <= 2 && L == 1;
   static_assert(!kPipe || (kAhead + 1) % 2 == 0, "tiles alternate between two accumulator sets");
 
@@ -585,10 +610,10 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     // the document, a tile's loads at offsets from it (rows past the end
     // read 0 and are masked), the document's constants once before its
     // tiles and its score once after them.
-    constexpr int kCodeBytes = DOC == kDocInt4 ? 64 : 16;
     const int ntok = (int)(de - ds);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.codes + ds * kCodeBytes, (uint32_t)ntok * kCodeBytes);
-    const __amdgpu_buffer_rsrc_t rr = make_rsrc(RES ? p.rcodes + ds * 64 : p.codes, RES ? (uint32_t)ntok * 64u : 0u);
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(RES ? p.rcodes + ds * kResBytes : p.codes, RES ? (uint32_t)ntok * (uint32_t)kResBytes : 0u);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.tscale + ds, (uint32_t)ntok * 4u);
     const __amdgpu_buffer_rsrc_t rsr = make_rsrc(RES ? p.rtscale + ds : p.tscale, RES ? (uint32_t)ntok * 4u : 0u);
     {
@@ -602,11 +627,14 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     auto fetch = [&](int i, Tile& t) __attribute__((always_inline)) {
       t.e = 0;
       const int row = 16 * i + c;
-      if constexpr (DOC == kDocInt4)
-        t.a.w = load_b128(ra, row * 64 + 16 * g);
-      else
-        t.a.w = load_b32(ra, row * 16 + 4 * g);
-      if constexpr (RES) t.r.w = load_b128(rr, row * 64 + 16 * g);
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        if constexpr (DOC == kDocInt4)
+          t.a.w[kc] = load_b128(ra, row * kCodeBytes + 64 * kc + 16 * g);
+        else
+          t.a.w[kc] = load_b32(ra, row * kCodeBytes + 16 * kc + 4 * g);
+        if constexpr (RES) t.r.w[kc] = load_b128(rr, row * kResBytes + 64 * kc + 16 * g);
+      }
       if constexpr (!INTMAX) {
         const v4u sv = load_b128(rs, (16 * i + 4 * g) * 4);
 #pragma unroll
@@ -661,29 +689,35 @@ __device__ __forceinline__ int query_byte(int d, int layout) {
   return 32 * g + 16 * (i >> 2) + 4 * (i & 3) + j;
 }
 
-// One wave per query row of 128 dims (lane l holds dims 2l, 2l + 1).
-// sigma = f32(max|q| / 127) (0 -> 1); limb l: a_l = clip(rint(r_l / s_l),
-// -127, 127), r_{l+1} = r_l - a_l s_l (one rounding), s_{l+1} = s_l / 254.
-// With `recip` (one limb) the quotient is q * (1 / sigma), the binary int8
-// query rounding of cu:1328-1366.  colmul = sigma; qsum[l] = sum of limb l.
-// With qpack2, the same codes also in layout2 (a cascade's two passes).
+// One wave per query row of 128 * chunks dims (lane l holds dims 128 kc +
+// 2l, 128 kc + 2l + 1 of each chunk kc; each chunk's bytes in the B-operand
+// order of a 128-dim row).  sigma = f32(max|q| / 127) over the whole row
+// (0 -> 1); limb l: a_l = clip(rint(r_l / s_l), -127, 127), r_{l+1} = r_l -
+// a_l s_l (one rounding), s_{l+1} = s_l / 254.  With `recip` (one limb) the
+// quotient is q * (1 / sigma), the binary int8 query rounding of
+// cu:1328-1366.  colmul = sigma; qsum[l] = sum of limb l.  With qpack2
+// (one chunk), the same codes also in layout2 (a cascade's two passes).
 __global__ __launch_bounds__(256) void quantize_limbs_kernel(const float* __restrict__ query, int64_t rows,
                                                              int64_t rows_padded, int limbs, int layout,
                                                              int recip, int8_t* __restrict__ qpack,
                                                              float* __restrict__ colmul,
                                                              int32_t* __restrict__ qsum, int layout2,
-                                                             int8_t* __restrict__ qpack2) {
+                                                             int8_t* __restrict__ qpack2, int chunks) {
+  constexpr int kMaxChunks = 4;
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= rows_padded) return;
+  const int64_t width = 128 * (int64_t)chunks;
   const int d0 = 2 * lane, d1 = 2 * lane + 1;
   const int p0 = query_byte(d0, layout), p1 = query_byte(d1, layout);
   const int p20 = query_byte(d0, layout2), p21 = query_byte(d1, layout2);
   if (row >= rows) {
     for (int l = 0; l < limbs; ++l) {
-      int8_t* dst = qpack + (l * rows_padded + row) * 128;
-      dst[p0] = 0;
-      dst[p1] = 0;
+      int8_t* dst = qpack + (l * rows_padded + row) * width;
+      for (int kc = 0; kc < chunks; ++kc) {
+        dst[128 * kc + p0] = 0;
+        dst[128 * kc + p1] = 0;
+      }
       if (qpack2) {
         int8_t* dst2 = qpack2 + (l * rows_padded + row) * 128;
         dst2[p20] = 0;
@@ -694,34 +728,45 @@ __global__ __launch_bounds__(256) void quantize_limbs_kernel(const float* __rest
     if (lane == 0) colmul[row] = 0.0f;
     return;
   }
-  const float2 v = reinterpret_cast<const float2*>(query + row * 128)[lane];
-  const float m = wave_reduce(fmaxf(fabsf(v.x), fabsf(v.y)), [](float x, float y) { return fmaxf(x, y); });
+  float rx[kMaxChunks], ry[kMaxChunks];
+  float mabs = 0.0f;
+#pragma unroll
+  for (int kc = 0; kc < kMaxChunks; ++kc) {
+    rx[kc] = ry[kc] = 0.0f;
+    if (kc < chunks) {
+      const float2 v = reinterpret_cast<const float2*>(query + row * width + 128 * kc)[lane];
+      rx[kc] = v.x;
+      ry[kc] = v.y;
+      mabs = fmaxf(mabs, fmaxf(fabsf(v.x), fabsf(v.y)));
+    }
+  }
+  const float m = wave_reduce(mabs, [](float x, float y) { return fmaxf(x, y); });
   const float sigma = m == 0.0f ? 1.0f : __fdiv_rn(m, 127.0f);
-  float rx = v.x, ry = v.y, s = sigma;
+  float s = sigma;
   for (int l = 0; l < limbs; ++l) {
-    float qx, qy;
-    if (recip) {
-      const float inv = __fdiv_rn(1.0f, s);
-      qx = rx * inv;
-      qy = ry * inv;
-    } else {
-      qx = __fdiv_rn(rx, s);
-      qy = __fdiv_rn(ry, s);
+    const float inv = recip ? __fdiv_rn(1.0f, s) : 0.0f;
+    int8_t* dst = qpack + (l * rows_padded + row) * width;
+    int lane_sum = 0;
+#pragma unroll
+    for (int kc = 0; kc < kMaxChunks; ++kc) {
+      if (kc >= chunks) break;
+      const float qx = recip ? rx[kc] * inv : __fdiv_rn(rx[kc], s);
+      const float qy = recip ? ry[kc] * inv : __fdiv_rn(ry[kc], s);
+      const int a = max(-127, min(127, (int)rintf(qx)));
+      const int b = max(-127, min(127, (int)rintf(qy)));
+      dst[128 * kc + p0] = (int8_t)a;
+      dst[128 * kc + p1] = (int8_t)b;
+      if (qpack2) {
+        int8_t* dst2 = qpack2 + (l * rows_padded + row) * 128;
+        dst2[p20] = (int8_t)a;
+        dst2[p21] = (int8_t)b;
+      }
+      lane_sum += a + b;
+      rx[kc] = fmaf(-(float)a, s, rx[kc]);
+      ry[kc] = fmaf(-(float)b, s, ry[kc]);
     }
-    const int a = max(-127, min(127, (int)rintf(qx)));
-    const int b = max(-127, min(127, (int)rintf(qy)));
-    int8_t* dst = qpack + (l * rows_padded + row) * 128;
-    dst[p0] = (int8_t)a;
-    dst[p1] = (int8_t)b;
-    if (qpack2) {
-      int8_t* dst2 = qpack2 + (l * rows_padded + row) * 128;
-      dst2[p20] = (int8_t)a;
-      dst2[p21] = (int8_t)b;
-    }
-    const int sum = wave_reduce(a + b, [](int x, int y) { return x + y; });
+    const int sum = wave_reduce(lane_sum, [](int x, int y) { return x + y; });
     if (lane == 0) qsum[l * rows_padded + row] = sum;
-    rx = fmaf(-(float)a, s, rx);
-    ry = fmaf(-(float)b, s, ry);
     s = s * kLimbStep;
   }
   if (lane == 0) colmul[row] = sigma;
@@ -768,7 +813,7 @@ __global__ __launch_bounds__(256) void pool_sum_kernel(const float* __restrict__
   if (iout) iout[b * targets + t] = (int32_t)sum;
 }
 
-template <int DOC, bool RES, int L, int NT>
+template <int DOC, bool RES, int L, int NT, int KC = 1>
 hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s) {
   if constexpr (DOC == kDocSign && !RES && L == 1) {
     if (reducer == kRedMax && a.unit_tscale) {
@@ -777,10 +822,10 @@ hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s)
     }
   }
   switch (reducer) {
-    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax, false><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2, false><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4, false><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse, false><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax, false, KC><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2, false, KC><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4, false, KC><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse, false, KC><<<grid, kThreads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -788,9 +833,12 @@ hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s)
 
 }  // namespace
 
-int score_rows_per_pass(int limbs, int64_t rows) {
-  // Three limbs keep at most four 16-row tiles of B operands in registers,
-  // one limb eight; small queries use two tiles.
+int score_rows_per_pass(int limbs, int64_t rows, int chunks) {
+  // Three limbs keep at most four 16-row tiles of B operands in registers
+  // per 128-dim chunk budget (two tiles at two chunks, one at four), one limb
+  // eight; small queries use two tiles.
+  if (chunks == 2) return 32;
+  if (chunks >= 4) return 16;
   const int max_nt = limbs == 3 ? 4 : 8;
   return 16 * (rows <= 32 ? 2 : max_nt);
 }
@@ -801,9 +849,26 @@ hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, i
     return hipErrorInvalidValue;
   if (a.tscale == nullptr || (residual && (a.rcodes == nullptr || a.rtscale == nullptr)))
     return hipErrorInvalidValue;
-  const int rpp = score_rows_per_pass(limbs, a.grp_rows);
+  const int chunks = a.chunks <= 0 ? 1 : a.chunks;
+  const int rpp = score_rows_per_pass(limbs, a.grp_rows, chunks);
   const int nt = rpp / 16;
   const dim3 grid((unsigned)(a.num_waves / kWavesPerGroup), (unsigned)(groups * a.subs));
+  if (chunks != 1) {
+    // Dims above 128: fp32 queries (three limbs) against int4 documents (with
+    // or without the int4 residual) or sign documents.
+    if (limbs != 3 || (doc == kDocSign && residual)) return hipErrorInvalidValue;
+    if (chunks == 2) {
+      if (doc == kDocInt4 && !residual) return launch_red<kDocInt4, false, 3, 2, 2>(a, reducer, grid, stream);
+      if (doc == kDocInt4) return launch_red<kDocInt4, true, 3, 2, 2>(a, reducer, grid, stream);
+      return launch_red<kDocSign, false, 3, 2, 2>(a, reducer, grid, stream);
+    }
+    if (chunks == 4) {
+      if (doc == kDocInt4 && !residual) return launch_red<kDocInt4, false, 3, 1, 4>(a, reducer, grid, stream);
+      if (doc == kDocInt4) return launch_red<kDocInt4, true, 3, 1, 4>(a, reducer, grid, stream);
+      return launch_red<kDocSign, false, 3, 1, 4>(a, reducer, grid, stream);
+    }
+    return hipErrorInvalidValue;
+  }
 #define MSIM_SCORE_NT(DOC, RES, L)                                              \
   return nt == 2 ? launch_red<DOC, RES, L, 2>(a, reducer, grid, stream)         \
                  : launch_red<DOC, RES, L, (L == 3 ? 4 : 8)>(a, reducer, grid, stream)
@@ -819,12 +884,14 @@ hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, i
 
 hipError_t launch_quantize_limbs(const float* d_query, int64_t rows, int64_t rows_padded, int limbs, int layout,
                                  bool recip, int8_t* qpack, float* colmul, int32_t* qsum, hipStream_t stream,
-                                 int layout2, int8_t* qpack2) {
+                                 int layout2, int8_t* qpack2, int chunks) {
   if (rows_padded <= 0) return hipSuccess;
+  if (chunks != 1 && chunks != 2 && chunks != 4) return hipErrorInvalidValue;
+  if (qpack2 && chunks != 1) return hipErrorInvalidValue;
   const int64_t blocks = (rows_padded + 3) / 4;
   quantize_limbs_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(d_query, rows, rows_padded, limbs, layout,
                                                                         recip ? 1 : 0, qpack, colmul, qsum,
-                                                                        qpack2 ? layout2 : layout, qpack2);
+                                                                        qpack2 ? layout2 : layout, qpack2, chunks);
   return hipGetLastError();
 }
 
