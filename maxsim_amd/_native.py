@@ -164,11 +164,12 @@ def check(status: int) -> None:
     raise RuntimeError(message)
 
 
-def ptr(array) -> ctypes.c_void_p | None:
-    """Address of a NumPy array's data or a torch tensor's storage (or None)."""
+def ptr(array) -> int | None:
+    """Address of a NumPy array's data or a torch tensor's storage (or None),
+    as an int (every pointer argument of the binding is a c_void_p)."""
     if array is None:
         return None
     data_ptr = getattr(array, "data_ptr", None)
     if data_ptr is not None:
-        return ctypes.c_void_p(data_ptr())
-    return array.ctypes.data_as(ctypes.c_void_p)
+        return data_ptr()
+    return array.__array_interface__["data"][0]

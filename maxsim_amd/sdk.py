@@ -465,5 +465,17 @@ def _format_candidate_row(scores, candidate_indices, candidate_ids, k: int):
             for r, p in enumerate(order, start=1)]
 
 
+_new_object = object.__new__
+_set_attribute = object.__setattr__
+
+
 def _format_result_row(scores, indices, doc_ids):
-    return [SearchResult(doc_ids[i], s, r) for r, (s, i) in enumerate(zip(scores, indices), start=1)]
+    # The frozen dataclass's fields set in one step (its generated __init__
+    # sets them one by one through object.__setattr__, about twice the time
+    # per result); the objects are the same SearchResult values.
+    out = []
+    for rank, (score, index) in enumerate(zip(scores, indices), start=1):
+        result = _new_object(SearchResult)
+        _set_attribute(result, "__dict__", {"doc_id": doc_ids[index], "score": score, "rank": rank})
+        out.append(result)
+    return out
