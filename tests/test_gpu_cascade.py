@@ -258,6 +258,49 @@ def test_binres_cascade_fp32_rescoring_equals_host_procedure(gpu, qt):
         np.testing.assert_array_equal(fs[b], full[b][fi[b]])
 
 
+def test_binres_fp32_cascade_config5_scale_against_oracle(gpu, oracle):
+    """The config-5 workload (4,096 documents of 64-192 tokens, query
+    [4, 32, 128]) with the fp32-query rescoring of M = 512 candidates:
+    * the fused fp32 scores of every document against the dense oracle over
+      the reconstructed tokens, at the fp32 bar (rtol 1e-5);
+    * the top-10 against the oracle pipeline (cascade.py:294-453): coarse
+      scores from the oracle's int8-query prefix scores (which the device
+      prefix pass equals bit for bit), stable top-512, dense fp32 rescoring
+      of those candidates, top-10 by (score desc, document id asc).  The
+      device's ten documents must be candidates of the oracle's coarse top-512
+      and carry, in order, the oracle's ten best rescored values (the device's
+      own fused scores agree with the oracle's to the fp32 bar, so documents
+      whose oracle scores tie within it may trade places)."""
+    from maxsim_amd import synthetic
+    from maxsim_amd.binres import binres_cascade_topk, binres_score
+
+    cfg = synthetic.CONFIGS[5]
+    corpus = synthetic.make_corpus(cfg["num_docs"], cfg["lo"], cfg["hi"], seed=55)
+    query = synthetic.make_queries(corpus, cfg["batch"], seed=56)
+    docs, offsets = corpus.embeddings, corpus.offsets
+    packed = _binres(docs, offsets)
+    signs, a, _, _, _ = oracle.pack_binary_residual(docs)
+    recon = _binres_recon(oracle, docs)
+    k, m = 10, 512
+    print("case: config-5 fp32 fused scores, 4096 docs", flush=True)
+    full = binres_score(query, packed, fused=True, query_precision="fp32")
+    _close(full, oracle.dense_scores(query, recon, offsets), 1e-5)
+    print("case: config-5 fp32-rescoring cascade, M=512", flush=True)
+    top_s, top_i = binres_cascade_topk(query, packed, k, candidates=m, query_precision="fp32")
+    coarse = oracle.binres_prefix_scores(query, signs, a, offsets)
+    for b in range(cfg["batch"]):
+        cands = np.sort(_stable(coarse[b], m))
+        fine = oracle.dense_scores(query[b:b + 1], recon, offsets, candidates=cands)[0]
+        exp_pos = _stable(fine, k, tie_ids=cands)
+        exp_scores = fine[exp_pos]
+        pos = np.searchsorted(cands, top_i[b])
+        assert np.all(pos < m) and np.array_equal(cands[pos], top_i[b]), "a result outside the coarse top-512"
+        _close(fine[pos], exp_scores, 1e-5)
+        _close(top_s[b], fine[pos], 1e-5)
+        overlap = len(set(top_i[b].tolist()) & set(cands[exp_pos].tolist()))
+        assert overlap >= k - 1, (b, overlap)
+
+
 def test_binres_rescore_limbs_validation(gpu):
     docs, offsets = ragged_fixture(20, 3, lo=1, hi=20)
     h = _binres(docs, offsets).sign_data
