@@ -70,6 +70,8 @@ def parse_args():
                     help="append plain device copies of known size (PMC calibration)")
     ap.add_argument("--pack", action="store_true",
                     help="measure the device int4 packer (index build) instead of a search config")
+    ap.add_argument("--rates", action="store_true",
+                    help="run the instruction-rate tests (maxsim_amd/microbench/rates.hip) instead of a search config")
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="BASELINE configuration to measure (2 = the headline metric)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -870,6 +872,41 @@ def bench_pack(args):
 
 OTHER_CONFIGS = {3: bench_config3, 4: bench_config4, 5: bench_config5}
 
+RATE_TESTS = ("mfma", "mfma_fma2", "mfma_fma3", "mfma_fma4", "mfma_fma6", "scan_tile", "xor_bcnt", "mfma_sign")
+
+
+def bench_rates(args):
+    """Instruction-rate tests (no memory traffic in the loops) on every CU,
+    with one and two waves per SIMD: nanoseconds per unit per SIMD (an MFMA
+    for the mfma* tests, a 16-token tile for scan_tile, a 128-bit (query row,
+    token) Hamming pair for xor_bcnt and mfma_sign), and chip-wide rates."""
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "maxsim_amd", "libmaxsim_rates.so"))
+    lib.msim_rate_test.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.POINTER(ctypes.c_double)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = {"xor_bcnt": 4000, "mfma_sign": 4000, "scan_tile": 2000}
+    out = {}
+    for name in RATE_TESTS:
+        row = {}
+        for wps in (1, 2):
+            ns = ctypes.c_double(0.0)
+            if lib.msim_rate_test(name.encode(), cus, wps, iters.get(name, 4000), ctypes.byref(ns)) != 0:
+                raise SystemExit(f"rate test {name} failed")
+            row[f"ns_per_unit_{wps}w"] = ns.value
+        simds = 4 * cus
+        if name.startswith("mfma") and name != "mfma_sign":
+            row["int8_tops_2w"] = 32768 * simds / row["ns_per_unit_2w"] / 1e3
+        if name in ("xor_bcnt", "mfma_sign"):
+            row["pairs_per_ns_chip_2w"] = simds / row["ns_per_unit_2w"]
+        out[name] = row
+        print(f"{name:10s} " + " ".join(f"{k}={v:.3f}" for k, v in row.items()), file=sys.stderr, flush=True)
+    return {"metric": "instruction-rate tests", "cus": cus, "tests": out,
+            "units": {"mfma*": "one v_mfma_i32_16x16x64_i8 (with its fmas)", "scan_tile": "one 16-token tile",
+                      "xor_bcnt": "one 128-dim (query row, token) pair", "mfma_sign": "one 128-dim pair"},
+            "metadata": host_metadata()}
+
 
 def main():
     args = parse_args()
@@ -881,7 +918,9 @@ def main():
               "scores on a single MI355X (documents would shard across GPUs with a top-k merge, not built here)",
               file=sys.stderr)
         sys.exit(2)
-    if args.pack:
+    if args.rates:
+        print(json.dumps(bench_rates(args)), flush=True)
+    elif args.pack:
         print(json.dumps(bench_pack(args)), flush=True)
     elif args.config == 2:
         bench_config2(args)

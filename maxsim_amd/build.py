@@ -15,6 +15,10 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmaxsim_hip.so")
+# Instruction-rate tests behind the scan's design (bench.py --rates): a
+# library of their own, not linked into the product.
+RATES_SRC = os.path.join(HERE, "microbench", "rates.hip")
+RATES_LIB = os.path.join(HERE, "libmaxsim_rates.so")
 ARCH = os.environ.get("MAXSIM_GPU_ARCH", "gfx950")
 
 FLAGS = [
@@ -59,10 +63,12 @@ def build(verbose: bool = False) -> str:
         cmds = [[hipcc, *compile_flags, "-c", s, "-o", o] for s, o in zip(srcs, objs)]
         if verbose:
             print(f"compiling {len(srcs)} sources with {jobs} jobs: " + " ".join(cmds[0][:-4]), flush=True)
+        rates_tmp = RATES_LIB + ".tmp"
+        cmds.append([hipcc, *FLAGS, RATES_SRC, "-o", rates_tmp])
         with ThreadPoolExecutor(max_workers=jobs) as pool:
             results = list(pool.map(_run, cmds))
         messages: list[str] = []
-        for src, (rc, lines) in zip(srcs, results):
+        for src, (rc, lines) in zip(srcs + [RATES_SRC], results):
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n" + "\n".join(lines))
             messages.extend(lines)
@@ -74,6 +80,7 @@ def build(verbose: bool = False) -> str:
     if verbose and messages:
         print("\n".join(messages))
     os.replace(tmp, LIB)
+    os.replace(rates_tmp, RATES_LIB)
     return LIB
 
 
