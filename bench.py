@@ -46,13 +46,14 @@ KERNEL_STATS = os.path.join(ROOT, "profiles", "int8q_scan_config2_kernel_stats.m
 MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # The achievable bound of the fused scan under its present design, from
 # measured constants: a tile's 16 MFMAs at the rate of an MFMA followed by
-# three VALU instructions with two waves per SIMD (a rate test with no memory
-# traffic: 11.6 ns per MFMA), plus the time until a wave's first tiles land
-# (median wave, per-wave s_memrealtime stamps: 1.4 us) and the tail from the
-# last wave's loop end to the end of the selection (stamps: 3.5 us).
-MIX_NS_PER_MFMA = 11.6
-RAMP_US = 1.4
-TAIL_US = 3.5
+# three VALU instructions with two waves per SIMD (bench.py --rates,
+# mfma_fma3: 11.43 ns per MFMA), plus the time until a wave's first tile
+# lands (median wave, per-wave s_memrealtime stamps of a timing copy of the
+# kernel: 2.4 us) and the tail from the last wave's loop end to the end of
+# the selection (the same stamps: 4.8 us).
+MIX_NS_PER_MFMA = 11.43
+RAMP_US = 2.4
+TAIL_US = 4.8
 
 
 def parse_args():

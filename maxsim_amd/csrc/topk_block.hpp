@@ -553,24 +553,64 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   };
   auto key_current = [&](uint64_t x) { return ((uint32_t)x & kTailTagMask) == ktag; };
 
+  // T of the lane maxima lmax: the largest lane maximum that k lane maxima
+  // reach (ties counted).  Each lane counts the lane maxima at least its own
+  // (broadcast reads of all 64 from LDS, independent compares); T is the
+  // largest maximum whose count reaches k.  T >= 1, so blocks without
+  // documents (maximum 0) are never hot.
+  lds_u32* lm = (lds_u32*)cand;
+  auto threshold = [&](uint32_t lmax) -> uint32_t {
+    lm[lane] = lmax;
+    wave_sync_lds();
+    int ge0 = 0, ge1 = 0;
+#pragma unroll
+    for (int j = 0; j < kWave; j += 8) {
+      const v4u q0 = *(const __attribute__((address_space(3))) v4u*)(lm + j);
+      const v4u q1 = *(const __attribute__((address_space(3))) v4u*)(lm + j + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ge0 += q0[e] >= lmax ? 1 : 0;
+        ge1 += q1[e] >= lmax ? 1 : 0;
+      }
+    }
+    const uint32_t tt = max(wave_reduce(ge0 + ge1 >= k ? lmax : 0u, [](uint32_t x, uint32_t y) { return max(x, y); }), 1u);
+    wave_sync_lds();
+    return tt;
+  };
+
   // Round trip 1: the records (out of range: 0; a block without documents
-  // still writes one), read until every word carries the tag.
+  // still writes one), read until every word carries the tag.  Once at
+  // most half the lanes still wait, T is computed ahead from the current
+  // records (stale words count as 0) while the next poll is in flight, each
+  // time the lane maxima changed: they only grow, and if none that changed
+  // since ends at or above that T, the final T is the same (the lane maxima
+  // at or above it are the same multiset).
   const __amdgpu_buffer_rsrc_t rr = make_rsrc(rec, (uint32_t)(3 * kTailBlocks * 8));
   uint64_t w0[kTailBlocksPerLane], w1[kTailBlocksPerLane];
   uint32_t third[kTailBlocksPerLane];
+  uint64_t ra[kTailBlocksPerLane], rb[kTailBlocksPerLane], rc[kTailBlocksPerLane];
+  auto issue_poll = [&]() {
+#pragma unroll
+    for (int j = 0; j < kTailBlocksPerLane; ++j) {
+      const int blk = lane + kWave * j;
+      ra[j] = load_b64_coherent(rr, blk * 8);
+      rb[j] = load_b64_coherent(rr, (kTailBlocks + blk) * 8);
+      rc[j] = load_b64_coherent(rr, (2 * kTailBlocks + blk) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  uint32_t t_ahead = 0, lmax_ahead = 0;  // t_ahead 0: none computed
+  issue_poll();
   for (;;) {
     uint32_t stale = 0;
 #pragma unroll
     for (int j = 0; j < kTailBlocksPerLane; ++j) {
-      const int blk = lane + kWave * j;
-      const uint64_t a = load_b64_coherent(rr, blk * 8);
-      const uint64_t b = load_b64_coherent(rr, (kTailBlocks + blk) * 8);
-      const uint64_t c = load_b64_coherent(rr, (2 * kTailBlocks + blk) * 8);
-      const bool in = blk < nblocks;
-      w0[j] = in ? a : 0ull;
-      w1[j] = in ? b : 0ull;
-      third[j] = in ? (uint32_t)(c >> 32) : 0u;
-      stale |= (uint32_t)in & ((uint32_t)!key_current(a) | (uint32_t)!key_current(b) | (uint32_t)((uint32_t)c != tag));
+      const bool in = lane + kWave * j < nblocks;
+      w0[j] = in ? ra[j] : 0ull;
+      w1[j] = in ? rb[j] : 0ull;
+      third[j] = in ? (uint32_t)(rc[j] >> 32) : 0u;
+      stale |= (uint32_t)in & ((uint32_t)!key_current(ra[j]) | (uint32_t)!key_current(rb[j]) |
+                               (uint32_t)((uint32_t)rc[j] != tag));
     }
     const uint64_t stale_lanes = __ballot(stale != 0);
     if (stale_lanes == 0) break;
@@ -579,36 +619,27 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
       return;
     }
     // Poll gently while many workgroups are still scanning (the polls take
-    // issue slots from the scan waves sharing this CU), then closely.
+    // issue slots from the scan waves sharing this CU), then closely, and
+    // compute T ahead when the current records changed it may.
     const int nstale = __popcll(stale_lanes);
+    uint32_t lf = 0;
+#pragma unroll
+    for (int j = 0; j < kTailBlocksPerLane; ++j) lf = max(lf, key_current(w0[j]) ? (uint32_t)(w0[j] >> 32) : 0u);
+    const bool ahead = nstale <= 32 && (t_ahead == 0 || __ballot(lf != lmax_ahead) != 0);
     if (nstale > 32) __builtin_amdgcn_s_sleep(32);
-    else if (nstale > 4) __builtin_amdgcn_s_sleep(8);
-    else __builtin_amdgcn_s_sleep(1);
+    else if (!ahead && nstale > 4) __builtin_amdgcn_s_sleep(8);
+    else if (!ahead) __builtin_amdgcn_s_sleep(1);
+    issue_poll();
+    if (ahead) {  // while the poll is in flight
+      lmax_ahead = lf;
+      t_ahead = threshold(lf);
+    }
   }
   uint32_t lmax = 0;
 #pragma unroll
   for (int j = 0; j < kTailBlocksPerLane; ++j) lmax = max(lmax, (uint32_t)(w0[j] >> 32));
-  // T: the largest lane maximum that k lane maxima reach (ties counted).
-  // Each lane counts the lane maxima at least its own (broadcast reads of
-  // all 64 from LDS, independent compares); T is the largest maximum whose
-  // count reaches k.  T >= 1, so blocks without documents (maximum 0) are
-  // never hot.
-  lds_u32* lm = (lds_u32*)cand;
-  lm[lane] = lmax;
-  wave_sync_lds();
-  int ge0 = 0, ge1 = 0;
-#pragma unroll
-  for (int j = 0; j < kWave; j += 8) {
-    const v4u q0 = *(const __attribute__((address_space(3))) v4u*)(lm + j);
-    const v4u q1 = *(const __attribute__((address_space(3))) v4u*)(lm + j + 4);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ge0 += q0[e] >= lmax ? 1 : 0;
-      ge1 += q1[e] >= lmax ? 1 : 0;
-    }
-  }
-  const uint32_t t = max(wave_reduce(ge0 + ge1 >= k ? lmax : 0u, [](uint32_t x, uint32_t y) { return max(x, y); }), 1u);
-  wave_sync_lds();
+  const bool ahead_holds = t_ahead != 0 && __ballot(lmax != lmax_ahead && lmax >= t_ahead) == 0;
+  const uint32_t t = ahead_holds ? t_ahead : threshold(lmax);
   // Per lane: its deep blocks (a third key >= T: all their keys are loaded;
   // bit j of dmask) and the record keys >= T of its other blocks (bits 2j,
   // 2j + 1 of cmask).  One scan gives every lane its offsets; each lane then
