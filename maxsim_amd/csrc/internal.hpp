@@ -132,6 +132,11 @@ constexpr int64_t kScanTailRow = 4096;  // key positions per batch row of the fu
 constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
 constexpr int kScanTailBlocks = 512;  // workgroups of a fused launch at most
 constexpr uint64_t kScanTailWaitTicks = 10000000;  // default wait of the fused selection: 100 ms
+// Launch tags repeat in the 19 tag bits of a key every kScanTailKeyPeriod
+// launches of one launch counter (tag % period + 1): the host zeroes the key
+// rows before every launch whose number is a multiple of the period, so a
+// key that carries the current tag was stored by the current launch.
+constexpr uint64_t kScanTailKeyPeriod = (1u << 19) - 1u;
 // Epilogue forms of the scan (the token scales decide which is exact):
 //  * kScanEpiIntMax: tensor-scale corpora (token_scale16 == nullptr): integer
 //    maximum of the dots, scaled at the document end;
