@@ -616,7 +616,24 @@ def bench_config3(args):
         ref = h.score_batch(query_np, red, w, tau)
         assert np.array_equal(scores.cpu().numpy(), ref), f"{red}: device-resident scores differ from the host API"
         wall, ev = _timed(step, args.steps, args.warmup, stream)
-        per[red] = {"ms_per_step": wall, "p50_ms": float(np.percentile(ev, 50)), "docs_per_s": b * n / (wall * 1e-3)}
+
+        def score_only():
+            check(lib.msim_int4_score_async(h._h, ptr(dq), b, q, red.encode(), ptr(w), 0 if w is None else 2,
+                                            0 if w is None else b, 0 if w is None else q, tau, 0, ptr(scores), sptr))
+
+        # The scoring launch alone: back-to-back launches between two events
+        # on the stream (each includes the launch-to-launch gap).
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(SCAN_BLOCK * 4):
+            score_only()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kernel_ms = e0.elapsed_time(e1) / (SCAN_BLOCK * 4)
+        int8_ops = 3 * 2.0 * b * q * t * 128
+        per[red] = {"ms_per_step": wall, "p50_ms": float(np.percentile(ev, 50)), "docs_per_s": b * n / (wall * 1e-3),
+                    "score_kernel_ms": kernel_ms,
+                    "mfma_frac": int8_ops / (kernel_ms * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS}
     # weighted MaxSim with new weights every step (two arrays alternating, so
     # the handle's unchanged-weights check never skips the upload)
     other = np.ascontiguousarray(weights[::-1])
