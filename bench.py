@@ -44,6 +44,7 @@ CALIBRATION_BYTES = 256 << 20  # one plain copy: reads and writes this many byte
 SCAN_BLOCK = 10  # scan launches between two events
 KERNEL_STATS = os.path.join(ROOT, "profiles", "int8q_scan_config2_kernel_stats.md")
 MFMA_INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+MFMA_FP4_PEAK_TOPS = 10100.0  # MI355X dense fp4 MFMA
 # The achievable bound of the fused scan under its present design, from
 # measured constants: a tile's 16 MFMAs at the rate of an MFMA followed by
 # three VALU instructions with two waves per SIMD (bench.py --rates,
@@ -719,13 +720,22 @@ def bench_config4(args):
     step()
     torch.cuda.synchronize()
     ref = h.hamming_batch(qbits[:8])
+    # The fp4 kernel against the int8 MFMA scorer on the same rows: equal.
+    _maxsim_hip.set_hamming_fp4(0)
+    try:
+        ref_int8 = h.hamming_batch(qbits[:8])
+    finally:
+        _maxsim_hip.set_hamming_fp4(1)
+    assert np.array_equal(ref, ref_int8), "fp4 and int8 Hamming scores differ"
     ref_ids = np.stack([np.lexsort((np.arange(n), -row))[:args.k] for row in ref])
     assert np.array_equal(ti.cpu().numpy()[:8], ref_ids), "device top-k disagrees with device scores"
     wall, ev = _timed(step, max(3, args.steps // 20), max(1, args.warmup // 10), stream)
     ops = 2.0 * b * q * t * 128
-    roof = {"kernel": "score_kernel (sign docs, +-1 query)", "bound": "mfma", "unit": "TOP/s",
-            "achieved": ops / (wall * 1e-3) / 1e12, "peak": MFMA_INT8_PEAK_TOPS,
-            "note": "step time (scan of 8,192 query rows + top-10); ops = 2 B Q T 128 int8"}
+    roof = {"kernel": "hamming_kernel (sign docs, +-1 query as fp4 on v_mfma_scale_f32_16x16x128_f8f6f4)",
+            "bound": "mfma", "unit": "TOP/s", "achieved": ops / (wall * 1e-3) / 1e12, "peak": MFMA_FP4_PEAK_TOPS,
+            "int8_peak_frac": ops / (wall * 1e-3) / 1e12 / MFMA_INT8_PEAK_TOPS,
+            "note": "step time (scan of 8,192 query rows + top-10); ops = 2 B Q T 128 (+-1 products) against "
+                    "the dense fp4 MFMA peak of the instruction used"}
     roof["frac"] = roof["achieved"] / roof["peak"]
     cpu = None
     if not args.no_cpu_baseline:
@@ -746,7 +756,7 @@ def bench_config4(args):
                "sample": f"1 of the 256 queries (32 tokens) x all {n} docs, {src}, 1 thread, {el:.1f} s"}
     return _result("docs scored/sec, binary sign-query XOR/popcount-equivalent full scan + top-10 (1 GPU)",
                    b * n / (wall * 1e-3), "docs scored/s", args, wall, float(np.percentile(ev, 50)),
-                   float(np.percentile(ev, 95)), "int8",
+                   float(np.percentile(ev, 95)), "fp4 (+-1)",
                    f"BASELINE config 4: {n} binary docs x U{{256..1024}} tokens ({t} tokens), 256 x 32 sign queries, "
                    "top-10",
                    {"roofline": roof, "cpu_baseline": cpu})

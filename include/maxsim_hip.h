@@ -71,6 +71,13 @@ int64_t msim_get_fused_wait_ticks(void);
  * counterpart in the reference, which has no such format. */
 int msim_set_prefix_scan(int mode);
 int msim_get_prefix_scan(void);
+/* Sign-query (Hamming) scoring of binary handles (msim_binary_hamming_batch,
+ * msim_binary_topk_hamming*): 1 (default) = the fp4 kernel (one
+ * v_mfma_scale_f32_16x16x128_f8f6f4 on +-1 fp4 operands per 16 tokens x 16
+ * query rows x 128 dims, 256 query rows per pass), 0 = the int8 MFMA scorer
+ * (tests both; results identical).  No counterpart in the reference. */
+int msim_set_hamming_fp4(int mode);
+int msim_get_hamming_fp4(void);
 /* Work split of the int8-query scan: 0 (default) = documents to waves
  * longest first, each to the least-loaded wave (whole corpus addressed from
  * one base; up to 2^25 tokens and 2^24 documents, beyond that as 1);

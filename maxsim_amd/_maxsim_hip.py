@@ -202,6 +202,16 @@ def get_prefix_scan() -> int:
     return int(_native.load().msim_get_prefix_scan())
 
 
+def set_hamming_fp4(mode: int) -> None:
+    """Sign-query (Hamming) scoring: 1 = the fp4 MFMA kernel (default), 0 = the
+    int8 MFMA scorer (testing); results are identical."""
+    check(_native.load().msim_set_hamming_fp4(int(mode)))
+
+
+def get_hamming_fp4() -> int:
+    return int(_native.load().msim_get_hamming_fp4())
+
+
 def set_scan_partition(mode: int) -> None:
     """Work split of the int8-query scan: 0 = longest-first document
     assignment (default), 1 = contiguous document ranges."""

@@ -37,6 +37,8 @@ SIGNATURES: dict[str, list] = {
     "msim_get_scan_partition": [],
     "msim_set_prefix_scan": [c_int],
     "msim_get_prefix_scan": [],
+    "msim_set_hamming_fp4": [c_int],
+    "msim_get_hamming_fp4": [],
     # int4 handle
     "msim_int4_create": [c_vp, c_i64, c_i64, c_vp, c_i64, c_int, c_dbl, c_vp],
     "msim_int4_destroy": [c_vp],

@@ -17,6 +17,7 @@ int g_docs_per_wave = 0;
 int g_fused_topk = 1;  // msim_set_fused_topk
 int g_scan_partition = 0;  // msim_set_scan_partition
 int g_scan_prefix = 1;     // msim_set_prefix_scan
+int g_hamming_fp4 = 1;     // msim_set_hamming_fp4
 uint64_t g_fused_wait_ticks = kScanTailWaitTicks;  // msim_set_fused_wait_ticks
 
 void set_error(const std::string& msg) { g_last_error = msg; }
@@ -142,6 +143,15 @@ extern "C" int msim_set_prefix_scan(int mode) {
 }
 
 extern "C" int msim_get_prefix_scan(void) { return g_scan_prefix; }
+
+extern "C" int msim_set_hamming_fp4(int mode) {
+  return guarded([&] {
+    if (mode < 0 || mode > 1) throw InvalidArgument("hamming fp4 mode must be 0 or 1");
+    g_hamming_fp4 = mode;
+  });
+}
+
+extern "C" int msim_get_hamming_fp4(void) { return g_hamming_fp4; }
 
 // -------------------------------------------------------------- int4 handle
 

@@ -26,6 +26,7 @@ struct NotSupported : std::runtime_error {
 
 extern thread_local std::string g_last_error;
 extern int g_docs_per_wave;
+extern int g_hamming_fp4;  // sign-query scoring: fp4 Hamming kernel (1) or the int8 MFMA scorer (0)
 extern int g_scan_prefix;  // binary-prefix cascades: prefix pass on the int8-query scan
 extern uint64_t g_fused_wait_ticks;  // msim_set_fused_wait_ticks
 

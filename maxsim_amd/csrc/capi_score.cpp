@@ -76,13 +76,18 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   if (chunks != 1 && (limbs != 3 || q.d_qbits || q.alt_int4 || q.from_alt || (s.doc == kDocSign && s.residual)))
     throw NotSupported("dims above 128 are scored for fp32 queries against int4 or sign documents only");
 
+  // Sign-bit queries against sign documents over every document, MaxSim on
+  // unit token scales: the fp4 Hamming kernel reads the query bits itself.
+  const bool fp4 = g_hamming_fp4 != 0 && q.d_qbits && s.doc == kDocSign && !s.residual && reducer == kRedMax &&
+                   s.unit_tscale && chunks == 1 && !t.host && !t.device && h_row_weights == nullptr;
+
   // 1. Quantise the query rows.
   ws.qpack.ensure((size_t)limbs * rows_padded * 128 * chunks, "hipMalloc query limbs");
   ws.colmul.ensure(sizeof(float) * rows_padded, "hipMalloc query scales");
   ws.qsum.ensure(sizeof(int32_t) * limbs * rows_padded, "hipMalloc query limb sums");
   if (q.alt_int4) ws.qpack_alt.ensure((size_t)limbs * rows_padded * 128, "hipMalloc query limbs (int4 layout)");
-  if (q.quantized || q.from_alt) {
-    // reuse the workspace's quantised rows
+  if (q.quantized || q.from_alt || fp4) {
+    // reuse the workspace's quantised rows (the fp4 kernel reads the bits)
   } else if (q.d_qbits)
     check_hip(launch_quantize_bits(q.d_qbits, rows, rows_padded, ws.qpack.as<int8_t>(), ws.colmul.as<float>(),
                                    ws.qsum.as<int32_t>(), stream),
@@ -112,7 +117,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   // 3. Work split.
   const int64_t groups = t.per_row ? batch : 1;
   const int64_t grp_rows = t.per_row ? query_tokens : rows;
-  const int64_t rpp = score_rows_per_pass(limbs, grp_rows, chunks);
+  const int64_t rpp = fp4 ? kHammingRowsPerPass : score_rows_per_pass(limbs, grp_rows, chunks);
   const int64_t subs = ceil_div(grp_rows, rpp);
   const int64_t per_target = t.per_row ? t.count : targets;
   int64_t waves = ceil_div((int64_t)device_cu_count() * 8, groups * subs);
@@ -213,6 +218,7 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
   a.unit_tscale = s.unit_tscale;
   a.query_tokens = (int32_t)query_tokens;
   a.chunks = chunks;
+  a.qbits = fp4 ? q.d_qbits : nullptr;
   // Passes that hold whole batch rows let the kernel sum them itself.
   const bool in_kernel_sum = t.per_row ? subs == 1 : rpp % query_tokens == 0;
   if (in_kernel_sum) {
@@ -220,13 +226,19 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
     a.out_stride = out_stride;
     a.iout = d_iout;
     a.iout_stride = per_target;
-    check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
+    if (fp4)
+      check_hip(launch_hamming(a, stream), "launch fp4 hamming kernel");
+    else
+      check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
     return;
   }
   ws.pooled.ensure(sizeof(float) * std::max<int64_t>(1, groups * per_target * grp_rows), "hipMalloc pooled rows");
   a.pooled = ws.pooled.as<float>();
   a.pooled_grp_stride = per_target * grp_rows;
-  check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
+  if (fp4)
+    check_hip(launch_hamming(a, stream), "launch fp4 hamming kernel");
+  else
+    check_hip(launch_score(a, s.doc, s.residual, limbs, reducer, groups, stream), "launch score kernel");
   const int64_t bs = t.per_row ? per_target * query_tokens : query_tokens;
   const int64_t ts = t.per_row ? query_tokens : rows;
   check_hip(launch_pool_sum(ws.pooled.as<float>(), batch, query_tokens, per_target, bs, ts, d_out, out_stride, d_iout,

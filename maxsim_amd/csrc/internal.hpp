@@ -226,7 +226,13 @@ struct ScoreArgs {
   int32_t query_tokens;
   bool unit_tscale;            // tscale is all ones (sign documents): integer maximum
   int32_t chunks;              // 128-dim chunks per token and query row (1, 2 or 4)
+  // Sign-bit queries [rows][16] (pack_signs order) scored against sign
+  // documents by the fp4 Hamming kernel (launch_hamming); null otherwise.
+  const uint8_t* qbits;
 };
+// Query rows per pass of the fp4 Hamming kernel (sixteen 16-row blocks).
+constexpr int kHammingRowsPerPass = 256;
+hipError_t launch_hamming(const ScoreArgs& a, hipStream_t stream);
 // Dims above 128 are scored in 128-dim chunks whose MFMA dots accumulate in
 // one int32 accumulator: 2 chunks up to 256 dims, 4 up to 512 (0: above).
 // 512 is the limit of the three-limb combination 254 a1 + a2 in int32

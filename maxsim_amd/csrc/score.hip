@@ -914,3 +914,156 @@ hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tok
 }
 
 }  // namespace msim
+
+// ------------------------------------------------------------ fp4 Hamming
+
+namespace msim {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// 32 sign bits of one lane (dims 32g .. 32g + 31, bit b = dim 32g + b; set =
+// +1) as the fp4 (e2m1) operand of v_mfma_scale_f32_16x16x128_f8f6f4: dword
+// q holds dims 32g + 4i + q in nibble i, +1 as 0x2 and -1 as 0xA.  Queries and
+// documents use the same dim order, so the MFMA's K order is irrelevant.
+__device__ __forceinline__ v4i fp4_signs(unsigned w) {
+  const unsigned n = ~w;
+  v4i a;
+  a[0] = (int)(0x22222222u | ((n << 3) & 0x88888888u));
+  a[1] = (int)(0x22222222u | ((n << 2) & 0x88888888u));
+  a[2] = (int)(0x22222222u | ((n << 1) & 0x88888888u));
+  a[3] = (int)(0x22222222u | (n & 0x88888888u));
+  return a;
+}
+
+__device__ __forceinline__ v4f mfma_fp4(const v4i& a, const v4i& b) {
+  typedef int v8i __attribute__((ext_vector_type(8)));
+  const v8i a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0}, b8 = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+  const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Formats 4 / 4: fp4 A and B; E8M0 scales 127 = 2^0.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b8, zero, 4, 4, 0, 127, 0, 127);
+}
+
+// MaxSim of sign-bit queries against sign documents, Hamming form: the +-1
+// dot q . d = 128 - 2 popcount(q ^ d) of each (query row, token), its maximum
+// over a document's tokens, summed over the query tokens of a batch row (the
+// sum cpu_extension.cpp:82-126 computes for +-1 queries; every value an
+// integer below 2^24, so float sums and maxima are exact).  One v_mfma_scale_f32_16x16x128_f8f6f4 on fp4 +-1
+// operands covers 16 tokens x 16 query rows x 128 dims (twice the K of the
+// int8 MFMA at the same issue rate), so a pass holds 256 query rows (NT = 16
+// blocks).  Table mode over every document (build_score_tables), tiles in a
+// ring of eight words per lane; rows past a short document read its last
+// token again, which leaves every maximum unchanged.
+template <int NT>
+__global__ __launch_bounds__(kThreads, 2) void hamming_kernel(ScoreArgs p) {
+  constexpr int kRing = 8;
+  __shared__ float s_pool[kWavesPerGroup][16 * NT];
+  const int lane = lane_id();
+  const int wave = wave_uniform(threadIdx.x / kWave);
+  const int g = lane >> 4, c = lane & 15;
+  const int sub = (int)blockIdx.y;
+  const int64_t gw = (int64_t)blockIdx.x * kWavesPerGroup + wave;
+  const auto info = as_constant(p.wave_info) + gw * kScoreInfoWords;
+  const int64_t t0 = info[0];
+  const int ntiles = (int)info[2];
+  if (ntiles == 0) return;
+  const auto tt = as_constant(p.tiles) + info[3];
+  const int lr0 = sub * 16 * NT;  // first query row of the pass
+
+  // Query operands: rows lr0 + 16 j + c (rows past the query read 0 bits).
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.qbits, (uint32_t)p.grp_rows * 16u);
+  v4i bq[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) bq[j] = fp4_signs(load_b32(rq, (lr0 + 16 * j + c) * 16 + 4 * g));
+
+  float m[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) m[j] = -1.0e30f;
+  int len = 0;
+
+  auto entry = [&](int i) -> uint64_t { return i < ntiles ? tt[i] : score_tile_entry(0, 1, false, false, 0); };
+  auto word = [&](uint64_t e) -> unsigned {
+    const int64_t start = (int64_t)(e & kTileStartMask);
+    const int rows1 = (int)((e >> kTileRowsShift) & 15);
+    return *reinterpret_cast<const unsigned*>(p.codes + (start + min(c, rows1)) * 16 + 4 * g);
+  };
+  auto finish = [&](int64_t tg) {
+    float v[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      float x = fmaxf(m[j], __shfl_xor(m[j], 16));
+      x = fmaxf(x, __shfl_xor(x, 32));
+      v[j] = len == 0 ? 0.0f : x * p.scale;
+      m[j] = -1.0e30f;
+    }
+    if (p.out || p.iout) {
+      if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) s_pool[wave][16 * j + c] = v[j];
+      }
+      wave_sync_lds();
+      const int nb = min(16 * NT, p.grp_rows - lr0) / p.query_tokens;
+      if (lane < nb) {
+        float sum = 0.0f;
+        for (int q = 0; q < p.query_tokens; ++q) sum += s_pool[wave][lane * p.query_tokens + q];
+        const int64_t b = lr0 / p.query_tokens + lane;
+        if (p.out) p.out[b * p.out_stride + tg] = sum;
+        if (p.iout) p.iout[b * p.iout_stride + tg] = (int32_t)sum;
+      }
+      wave_sync_lds();
+    } else {
+      float* out = p.pooled + tg * p.grp_rows;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int lr = lr0 + 16 * j + c;
+        if (g == 0 && lr < p.grp_rows) out[lr] = v[j];
+      }
+    }
+    len = 0;
+  };
+
+  // Ring: tile i's word in slot i % kRing, loaded kRing tiles ahead.  A
+  // tile's maxima wait behind the MFMA-result fence (two accumulator sets,
+  // one tile old, would spill at 256 query rows per pass).
+  uint64_t es[kRing];
+  unsigned ws[kRing];
+#pragma unroll
+  for (int u = 0; u < kRing; ++u) {
+    es[u] = entry(u);
+    ws[u] = word(es[u]);
+  }
+  for (int i0 = 0; i0 < ntiles; i0 += kRing) {
+#pragma unroll
+    for (int u = 0; u < kRing; ++u) {
+      if (i0 + u >= ntiles) break;
+      const uint64_t e = es[u];
+      const unsigned w = ws[u];
+      es[u] = entry(i0 + u + kRing);
+      ws[u] = word(es[u]);
+      if (((e >> kTileEmptyShift) & 1) == 0) {
+        const v4i a = fp4_signs(w);
+        v4f acc[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[j] = mfma_fp4(a, bq[j]);
+        mfma_results_fence();
+#pragma unroll
+        for (int j = 0; j < NT; ++j) m[j] = fmaxf(fmaxf(m[j], fmaxf(acc[j][0], acc[j][1])), fmaxf(acc[j][2], acc[j][3]));
+        len += (int)((e >> kTileRowsShift) & 15) + 1;
+      }
+      if ((e >> kTileLastShift) & 1) finish(t0 + (int64_t)(e >> kTileLocalShift));
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_hamming(const ScoreArgs& a, hipStream_t stream) {
+  if (a.num_waves <= 0 || a.num_waves % kWavesPerGroup != 0 || a.subs <= 0 || a.qbits == nullptr ||
+      a.wave_info == nullptr || a.tiles == nullptr)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(a.num_waves / kWavesPerGroup), (unsigned)a.subs);
+  hamming_kernel<kHammingRowsPerPass / 16><<<grid, kThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace msim

@@ -439,3 +439,33 @@ def test_scores_repeat_and_agree_across_row_splits(gpu, reducer):
             for _ in range(3):
                 rows = np.stack([binres_score(query[r:r + 1], b, fused=fused)[0] for r in range(4)])
                 np.testing.assert_array_equal(rows, ref)
+
+
+@pytest.fixture
+def hamming_fp4():
+    from maxsim_amd import _maxsim_hip
+
+    yield _maxsim_hip.set_hamming_fp4
+    _maxsim_hip.set_hamming_fp4(1)
+
+
+@pytest.mark.parametrize("mode", [1, 0])
+@pytest.mark.parametrize("shape", [(3, 9), (5, 40), (9, 32), (1, 300)])
+def test_hamming_fp4_and_int8_forms_bit_exact(gpu, oracle, hamming_fp4, mode, shape):
+    """Sign-query MaxSim on the fp4 kernel (mode 1: 256 query rows per pass,
+    +-1 fp4 operands) and on the int8 scorer (mode 0) against the oracle's
+    Hamming MaxSim, bit for bit: passes that hold whole batch rows (the
+    kernel sums them) and passes that do not (rows summed afterwards), short
+    and long documents and an empty one."""
+    print(f"case: hamming mode={mode} shape={shape}", flush=True)
+    hamming_fp4(mode)
+    docs, offsets = ragged_fixture(150, 61 + shape[1], lo=1, hi=70)
+    q = np.random.default_rng(62 + shape[0]).standard_normal((*shape, 128)).astype(np.float32)
+    qbits = oracle.pack_signs(q.reshape(-1, 128)).reshape(*shape, 16)
+    codes, h = _binary_handle(oracle, docs, offsets)
+    exp = oracle.binary_hamming_maxsim(qbits, codes, offsets, 128)
+    np.testing.assert_array_equal(h.hamming_batch(qbits), exp)
+    top_s, top_i = h.topk_hamming(qbits, 7)
+    ref_s, ref_i = oracle.topk(exp.astype(np.float32), 7)
+    np.testing.assert_array_equal(top_i, ref_i)
+    np.testing.assert_array_equal(top_s, ref_s)
