@@ -15,8 +15,9 @@ struct ScoreWorkspace {
   DeviceBuffer qpack_alt;  // the query also in the int4 layout (QueryInput::alt_int4)
   std::vector<float> weights_host;  // what `weights` holds (a repeated weight vector is not copied again)
   DeviceBuffer full_info, full_tiles;  // cached whole-corpus tables
-  int64_t full_key = -1;               // wave count the cached tables were built for
-  int64_t full_waves = 0;              // waves in the cached table
+  int64_t full_key = -1;               // wave count the cached tables were built for (units: -2 - workgroups)
+  int64_t full_waves = 0;              // records in the cached table
+  int64_t full_units = 0;              // records per workgroup (work-unit tables), else 0
   DeviceBuffer cand_ids, cand_info, cand_tiles;
   // cascade: coarse scores, top-M candidates (scores / ids), fine scores
   DeviceBuffer coarse, top_m_scores, top_m_ids, fine;

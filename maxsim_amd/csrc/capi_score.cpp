@@ -153,18 +153,29 @@ void run_generic_score(ScoreWorkspace& ws, const std::vector<int64_t>& off, int6
       a.info_grp_stride = w4 * kScoreInfoWords;
     }
   } else if (!t.host) {
-    if (ws.full_key != waves) {
+    // The row-block pipeline kernels (three limbs, four 16-row blocks per
+    // pass, one 128-dim chunk, no residual) take work units: a list per
+    // workgroup of eight waves, about `waves` waves in all.
+    const bool unit_tables = !fp4 && limbs == 3 && rpp == 64 && chunks == 1 && !s.rcodes &&
+                             num_docs < kScoreMaxUnitTargets;
+    const int64_t key = unit_tables ? -2 - ceil_div(waves, 8) : waves;
+    if (ws.full_key != key) {
       std::vector<int64_t> info;
       std::vector<uint64_t> tiles;
-      build_score_tables(off.data(), nullptr, num_docs, waves, info, tiles);
+      ws.full_units = 0;
+      if (unit_tables)
+        ws.full_units = build_score_units(off.data(), nullptr, num_docs, ceil_div(waves, 8), info, tiles);
+      else
+        build_score_tables(off.data(), nullptr, num_docs, waves, info, tiles);
       upload_vec(ws.full_info, info, "copy score wave table to device", stream);
       upload_vec(ws.full_tiles, tiles, "copy score tile table to device", stream);
-      ws.full_key = waves;
+      ws.full_key = key;
       ws.full_waves = (int64_t)info.size() / kScoreInfoWords;
     }
     a.wave_info = ws.full_info.as<int64_t>();
     a.tiles = ws.full_tiles.as<uint64_t>();
     a.num_waves = ws.full_waves;
+    a.group_units = (int32_t)ws.full_units;
     a.info_grp_stride = 0;
   } else {
     // Per group: its own table, all padded to the same wave count.

@@ -194,6 +194,12 @@ struct ScoreArgs {
   float rmul;
   const int64_t* wave_info;    // [groups][num_waves][kScoreInfoWords]
   const uint64_t* tiles;
+  // Work units (row-block pipeline kernels, eight waves per workgroup): 0 =
+  // wave w of a group takes record w of wave_info; n > 0 = workgroup x of a
+  // group owns records [n x, n x + n) (num_waves = n x workgroups), taken by
+  // its waves one after another from a counter in LDS; a record with no
+  // tiles ends the workgroup's list.
+  int32_t group_units;
   // Direct mode (wave_info / tiles unused): wave w of a group scores target w
   // (w < direct_count), the document targets[w] whose tokens are
   // [direct_offsets[doc], direct_offsets[doc + 1]).
@@ -254,6 +260,17 @@ hipError_t launch_pool_sum(const float* pooled, int64_t batch, int64_t query_tok
 // over about `waves` waves, balanced by tiles + 1 per target.
 void build_score_tables(const int64_t* offsets, const int64_t* targets, int64_t num_targets, int64_t waves,
                         std::vector<int64_t>& info, std::vector<uint64_t>& tiles);
+// Work units of the row-block pipeline kernels (ScoreArgs::group_units): the
+// targets balanced over `workgroups` lists (tiles + 1 per target, longest
+// first onto the least-loaded list), each list cut into units of whole
+// targets, longest first, every unit but the list's last of at least
+// kScoreUnitMinTiles tiles; lists padded with empty records to the same
+// count, which is returned.  Tile entries hold absolute target indices, so
+// num_targets must be below 2^24 (kScoreMaxUnitTargets).
+constexpr int64_t kScoreUnitMinTiles = 4;
+constexpr int64_t kScoreMaxUnitTargets = int64_t(1) << 24;
+int64_t build_score_units(const int64_t* offsets, const int64_t* targets, int64_t num_targets, int64_t workgroups,
+                          std::vector<int64_t>& info, std::vector<uint64_t>& tiles);
 
 // Cascade helpers (cascade.hip): tile tables of per-group candidate lists
 // written on the device (groups x waves waves of at most per_wave

@@ -185,25 +185,60 @@ __device__ __forceinline__ void unpack_a_int4_order(unsigned w, v4i& a0, v4i& a1
   }
 }
 
+// Three limbs, four row blocks, one stream: the row-block pipeline in table
+// mode (direct mode keeps the tile ring), in workgroups of eight waves, two
+// per SIMD, that share a list of work units.
+constexpr bool score_block_pipe(int nt, int limbs, bool res, int kc) { return nt > 2 && limbs == 3 && !res && kc == 1; }
+constexpr int score_group_waves(int nt, int limbs, bool res, int kc) {
+  return score_block_pipe(nt, limbs, res, kc) ? 8 : kWavesPerGroup;
+}
+
 // INTMAX (sign documents, one int8 limb, no token scale, MaxSim): the
 // +-1 dot 2 (q8 . bits) - sum(q8) is increasing in the MFMA result, so the
 // running maximum is kept on the int32 accumulators and converted once per
 // document.  KC: 128-dim chunks per token (dims above 128), each two more
 // MFMAs into the same accumulators.
 template <int DOC, bool RES, int L, int NT, int RED, bool INTMAX, int KC = 1>
-__global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreArgs p) {
+__global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 ? 2 : 1) void score_kernel(
+    ScoreArgs p) {
   static_assert(!INTMAX || (DOC == kDocSign && !RES && L == 1 && RED == kRedMax), "integer maximum form");
   static_assert(KC == 1 || (L == 3 && !(DOC == kDocSign && RES)), "chunked dims: fp32 queries, one document format");
   constexpr int kCodeBytes = (DOC == kDocInt4 ? 64 : 16) * KC;  // bytes per token of `codes`
   constexpr int kResBytes = 64 * KC;                            // and of `rcodes`
   constexpr int kQueryBytes = 128 * KC;                          // bytes per query row of a limb
-  __shared__ float s_pool[kWavesPerGroup][16 * NT];
+  constexpr bool kBlockPipe = score_block_pipe(NT, L, RES, KC);
+  constexpr int kGroupWaves = score_group_waves(NT, L, RES, KC);
+  __shared__ float s_pool[kGroupWaves][16 * NT];
   const int lane = lane_id();
   const int wave = wave_uniform(threadIdx.x / kWave);
   const int g = lane >> 4, c = lane & 15;
   const int grp = (int)blockIdx.y / p.subs, sub = (int)blockIdx.y % p.subs;
-  const int64_t gw = (int64_t)blockIdx.x * kWavesPerGroup + wave;
+  const int64_t gw = (int64_t)blockIdx.x * kGroupWaves + wave;
   const auto targets = p.targets ? as_constant(p.targets) + grp * p.targets_grp_stride : nullptr;
+  const int lr0 = sub * 16 * NT;                           // first local row of the pass
+  const int64_t grow0 = (int64_t)grp * p.grp_rows + lr0;  // its global query row
+
+  // Row-block pipeline: the waves of a workgroup share one pass of query
+  // rows, so its B operands are read from global memory once per workgroup,
+  // as whole 128-byte rows, and each wave takes its registers from LDS
+  // (before any wave may leave).  s_next counts the work units taken.
+  constexpr int kStageVecs = kBlockPipe ? L * NT * 2 * kWave : 1;
+  __shared__ v4i s_bq[kStageVecs];
+  __shared__ int s_next;
+  if constexpr (kBlockPipe) {
+    if (threadIdx.x == 0) s_next = 0;
+    // Piece x: 16 bytes at 16 (x % 8) of limb row x / 8 (limb l = row /
+    // (16 NT), local row 16 j + c); bytes 32 g + 16 h are lane 16 g + c's
+    // operand h of row block j.
+    for (int x = (int)threadIdx.x; x < kStageVecs; x += kGroupWaves * kWave) {
+      const int piece = x & 7, row = x >> 3;
+      const int l = row / (16 * NT), lr = row % (16 * NT);
+      const v4i v = *reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + grow0 + lr) * 128 + 16 * piece);
+      s_bq[((l * NT + lr / 16) * 2 + (piece & 1)) * kWave + (piece >> 1) * 16 + (lr & 15)] = v;
+    }
+    __syncthreads();
+  }
+
   // Table mode: the wave's first target, tile count and tiles from the
   // tables.  Direct mode: target gw of the group, its tiles from the token
   // range of its document.
@@ -218,7 +253,11 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     ds = as_constant(p.direct_offsets)[doc];
     de = as_constant(p.direct_offsets)[doc + 1];
     ntiles = ds == de ? 1 : (int)((de - ds + 15) / 16);
+  } else if (kBlockPipe && p.group_units > 0) {
+    t0 = 0;  // work units: taken below; tile entries hold absolute targets
+    ntiles = 0;
   } else {
+    if (gw >= p.num_waves) return;  // the last workgroup's waves past the table
     const auto info = as_constant(p.wave_info) + grp * p.info_grp_stride + gw * kScoreInfoWords;
     t0 = info[0];
     ntiles = (int)info[2];
@@ -234,8 +273,6 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     return score_tile_entry(x, min<int64_t>(16, de - x), x + 16 >= de, false, 0);
   };
   const auto doc_scale = p.doc_scale ? as_constant(p.doc_scale) : nullptr;
-  const int lr0 = sub * 16 * NT;                           // first local row of the pass
-  const int64_t grow0 = (int64_t)grp * p.grp_rows + lr0;  // its global query row
 
   // Query B operands and per-column constants.
   v4i bq[L][NT][KC][2];
@@ -248,9 +285,15 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     for (int l = 0; l < L; ++l) {
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const v4i* src = reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + r) * kQueryBytes + 128 * kc + 32 * g);
-        bq[l][j][kc][0] = src[0];
-        bq[l][j][kc][1] = src[1];
+        if constexpr (kBlockPipe) {
+          bq[l][j][kc][0] = s_bq[((l * NT + j) * 2 + 0) * kWave + lane];
+          bq[l][j][kc][1] = s_bq[((l * NT + j) * 2 + 1) * kWave + lane];
+        } else {
+          const v4i* src =
+              reinterpret_cast<const v4i*>(p.qpack + (l * p.rows_padded + r) * kQueryBytes + 128 * kc + 32 * g);
+          bq[l][j][kc][0] = src[0];
+          bq[l][j][kc][1] = src[1];
+        }
       }
       qsum[l][j] = DOC == kDocSign ? p.qsum[l * p.rows_padded + r] : 0;
     }
@@ -368,6 +411,45 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     }
     return ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
   };
+  // Similarity of token row 4g + rr (accumulator row rr) and column c of row
+  // block j.  `add` joins the first product in its rounding: -0 leaves it
+  // unchanged (x + -0 = x for every x, signed zeros included), -inf masks
+  // the row.
+  auto zval = [&](const Acc& A, const Pend& P, int j, int rr, float add) __attribute__((always_inline)) {
+    // Limb dots combined smallest first; sign documents recover the +-1 dot
+    // as 2 (q . bits) - sum(q).
+    // int4 documents with three limbs: the two small limbs first as one
+    // exact integer, 254 a1 + a2 (|a| <= 128 * 127 * 128 KC < 2^23 for
+    // KC <= 4, so the 24-bit multiply and the int32 sum are exact).
+    auto limbs3 = [&](const v4i (&a)[L][NT]) {
+      const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
+      return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
+    };
+    float Y;
+    if constexpr (L == 3 && DOC == kDocInt4) {
+      Y = limbs3(A.s);
+    } else {
+      float y[L];
+#pragma unroll
+      for (int l = 0; l < L; ++l)
+        // Sign documents: 2 (q . bits) - sum(q) as one fma on the
+        // converted dot (every term an integer below 2^24: exact).
+        y[l] = DOC == kDocSign ? fmaf((float)A.s[l][j][rr], 2.0f, (float)-qsum[l][j]) : (float)A.s[l][j][rr];
+      Y = y[0];
+      if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
+    }
+    float z = fmaf(Y, P.s[rr] * p.tmul, add);
+    if constexpr (RES) {
+      float YR;
+      if constexpr (L == 3) {
+        YR = limbs3(A.r);
+      } else {
+        YR = (float)A.r[0][j][rr];
+      }
+      z = z + YR * (P.sr[rr] * p.rmul);
+    }
+    return z;
+  };
   // Epilogue of row block j of a tile.
   auto epi_j = [&](const Acc& A, const Pend& P, int rows, int j) __attribute__((always_inline)) {
     if constexpr (INTMAX) {
@@ -381,41 +463,7 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     } else {
       float z[4];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        // Limb dots combined smallest first; sign documents recover the
-        // +-1 dot as 2 (q . bits) - sum(q).
-        // int4 documents with three limbs: the two small limbs first as one
-        // exact integer, 254 a1 + a2 (|a| <= 128 * 127 * 128 KC < 2^23 for
-        // KC <= 4, so the 24-bit multiply and the int32 sum are exact).
-        auto limbs3 = [&](const v4i (&a)[L][NT]) {
-          const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
-          return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
-        };
-        float Y;
-        if constexpr (L == 3 && DOC == kDocInt4) {
-          Y = limbs3(A.s);
-        } else {
-          float y[L];
-#pragma unroll
-          for (int l = 0; l < L; ++l)
-            // Sign documents: 2 (q . bits) - sum(q) as one fma on the
-            // converted dot (every term an integer below 2^24: exact).
-            y[l] = DOC == kDocSign ? fmaf((float)A.s[l][j][rr], 2.0f, (float)-qsum[l][j])
-                                   : (float)A.s[l][j][rr];
-          Y = y[0];
-          if constexpr (L == 3) Y = fmaf(fmaf(y[2], kLimbStep, y[1]), kLimbStep, y[0]);
-        }
-        z[rr] = Y * (P.s[rr] * p.tmul);
-        if constexpr (RES) {
-          float YR;
-          if constexpr (L == 3) {
-            YR = limbs3(A.r);
-          } else {
-            YR = (float)A.r[0][j][rr];
-          }
-          z[rr] = z[rr] + YR * (P.sr[rr] * p.rmul);
-        }
-      }
+      for (int rr = 0; rr < 4; ++rr) z[rr] = zval(A, P, j, rr, -0.0f);
       if (rows < 16) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
@@ -651,8 +699,143 @@ __global__ __launch_bounds__(kThreads, NT == 8 ? 2 : 1) void score_kernel(ScoreA
     run_ring(ntiles, fetch, meta, done);
     len = ntok;
     finish_target(t0);
+  } else if constexpr (kBlockPipe) {
+    // Row-block pipeline over a stream of tiles.  Step (i, j) issues the 2L
+    // MFMAs of row block j of tile i, each followed by a quarter of the
+    // epilogue of the row block two steps back: block j - 2 of tile i, or
+    // block NT - 2 + j of tile i - 1.  Its accumulators are then at least 2L
+    // MFMAs old (no fence needed), and the matrix core and the VALU work at
+    // once within the wave.  Row block j keeps accumulator set j: block
+    // j - 2's epilogue reads set j - 2 while set j is written, and set j is
+    // rewritten (tile i + 1) only after block j's epilogue (step j + 2, or
+    // step j + 2 - NT of tile i + 1).  A tile's masked rows (past a short
+    // document) get -inf in the same rounding as their product (the fma
+    // addend of zval).  Tiles in flight: a ring of kRing, the loads of tile
+    // i + kRing - 1 issued before tile i is computed.
+    //
+    // The stream: the wave's table (static tables), or the work units it
+    // takes from its workgroup's list (group_units > 0): unit A holds the
+    // current tile, unit B the next one, taken as A starts.  Every unit but
+    // a workgroup's last has at least kRing - 1 tiles, so the tiles loaded
+    // ahead lie in A or B.  The two waves of a SIMD do not share it evenly
+    // (the older wave issues first); taking units as they go, both finish
+    // with the workgroup's list.
+    constexpr int kRing = 4;
+    const bool units = p.group_units > 0;
+    const auto unit_info = as_constant(p.wave_info) + grp * p.info_grp_stride +
+                           (int64_t)blockIdx.x * p.group_units * kScoreInfoWords;
+    using TilePtr = const __attribute__((address_space(4))) uint64_t*;
+    auto take = [&](TilePtr& tp, int& n) __attribute__((always_inline)) {
+      int k = 0;
+      if (lane == 0) k = atomicAdd(&s_next, 1);
+      k = __builtin_amdgcn_readfirstlane(k);
+      n = 0;
+      if (k < p.group_units) {
+        const auto rec = unit_info + (int64_t)k * kScoreInfoWords;
+        n = (int)rec[2];
+        tp = as_constant(p.tiles) + rec[3];
+      }
+    };
+    TilePtr ta = tt, tb = nullptr;
+    int na = ntiles, nb = 0, base = 0;
+    if (units) {
+      take(ta, na);
+      if (na == 0) return;  // no barriers below
+      take(tb, nb);
+    }
+    auto entry_s = [&](int pos) -> uint64_t {
+      int q = pos - base;
+      if (q < na) return ta[q];
+      q -= na;
+      if (q < nb) return tb[q];
+      return score_tile_entry(0, 1, false, false, 0);
+    };
+    Tile ring[kRing];
+#pragma unroll
+    for (int u = 0; u < kRing - 1; ++u) load(entry_s(u), ring[u]);
+    Acc A;
+    Pend Pc, Pp;
+    float mc[4], mp[4];
+    int rows_c = 0, rows_p = 0;
+    auto mask_of = [&](int rows, float (&m)[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) m[rr] = 4 * g + rr >= rows ? kNegInf : -0.0f;
+    };
+    auto step = [&](const Ops& o, int jq, bool epi, const Pend& P, const float (&m)[4], int jp)
+                    __attribute__((always_inline)) {
+      const v4i zero = {0, 0, 0, 0};
+      float z[4];
+#pragma unroll
+      for (int k = 0; k < 2 * L; ++k) {
+        const int l = k % L, h = k / L;
+        A.s[l][jq] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][jq][0][h], h ? A.s[l][jq] : zero,
+                                                          0, 0, 0);
+        if (epi && k < 4) z[k] = zval(A, P, jp, k, m[k]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (epi) st[jp].add4(z, k2);
+    };
+    // Steps 0 .. NT - 1 of a tile (FIRST: tile 0, no previous tile).
+    auto tile_steps = [&](auto first_c, const Tile& t) __attribute__((always_inline)) {
+      constexpr bool kFirst = decltype(first_c)::value;
+      const Ops o = unpack(t);
+      Pc = pend_of(t);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (j < 2) {
+          step(o, j, !kFirst, Pp, mp, NT - 2 + j);
+          if (!kFirst && j == 1) end_tile(Pp, rows_p);
+        } else {
+          if (j == 2) {
+            rows_c = begin_tile(Pc);
+            mask_of(rows_c, mc);
+          }
+          step(o, j, true, Pc, mc, j - 2);
+        }
+      }
+      Pp = Pc;
+      rows_p = rows_c;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) mp[rr] = mc[rr];
+    };
+    // Tile i is in slot i % kRing; tile i + kRing - 1 goes to the slot of
+    // tile i - 1, whose steps are done.
+    load(entry_s(kRing - 1), ring[kRing - 1]);
+    tile_steps(std::integral_constant<bool, true>(), ring[0]);
+    for (int i0 = 1;; i0 += kRing) {
+      bool done = false;
+#pragma unroll
+      for (int u = 0; u < kRing; ++u) {
+        const int i = i0 + u;
+        if (i - base >= na) {  // unit A done: B follows
+          if (nb == 0) {
+            done = true;
+            break;
+          }
+          base += na;
+          ta = tb;
+          na = nb;
+          nb = 0;
+          if (units) take(tb, nb);
+        }
+        load(entry_s(i + kRing - 1), ring[u]);
+        tile_steps(std::integral_constant<bool, false>(), ring[(u + 1) % kRing]);
+      }
+      if (done) break;
+    }
+    // The last tile's blocks NT - 2 and NT - 1, right after their MFMAs.
+    mfma_results_fence();
+#pragma unroll
+    for (int j = NT - 2; j < NT; ++j) {
+      float z[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) z[rr] = zval(A, Pp, j, rr, mp[rr]);
+      st[j].add4(z, k2);
+    }
+    end_tile(Pp, rows_p);
   } else if constexpr (NT > 2) {
-    // Eight row blocks: a tight loop over the table's tiles, one in flight.
+    // Eight row blocks (one limb): a tight loop over the table's tiles, one
+    // in flight.
     Tile cur, nxt;
     uint64_t e = tt[0];
     load(e, cur);
@@ -815,17 +998,22 @@ __global__ __launch_bounds__(256) void pool_sum_kernel(const float* __restrict__
 
 template <int DOC, bool RES, int L, int NT, int KC = 1>
 hipError_t launch_red(const ScoreArgs& a, int reducer, dim3 grid, hipStream_t s) {
+  // Workgroups of kGroupWaves waves (the last one's waves past num_waves leave).
+  constexpr int kGroupWaves = score_group_waves(NT, L, RES, KC);
+  constexpr int kThr = kGroupWaves * kWave;
+  grid.x = (unsigned)(a.group_units > 0 ? a.num_waves / a.group_units : (a.num_waves + kGroupWaves - 1) / kGroupWaves);
+  if (a.group_units > 0 && !score_block_pipe(NT, L, RES, KC)) return hipErrorInvalidValue;
   if constexpr (DOC == kDocSign && !RES && L == 1) {
     if (reducer == kRedMax && a.unit_tscale) {
-      score_kernel<DOC, RES, L, NT, kRedMax, true><<<grid, kThreads, 0, s>>>(a);
+      score_kernel<DOC, RES, L, NT, kRedMax, true><<<grid, kThr, 0, s>>>(a);
       return hipGetLastError();
     }
   }
   switch (reducer) {
-    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax, false, KC><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2, false, KC><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4, false, KC><<<grid, kThreads, 0, s>>>(a); break;
-    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse, false, KC><<<grid, kThreads, 0, s>>>(a); break;
+    case kRedMax: score_kernel<DOC, RES, L, NT, kRedMax, false, KC><<<grid, kThr, 0, s>>>(a); break;
+    case kRedTop2: score_kernel<DOC, RES, L, NT, kRedTop2, false, KC><<<grid, kThr, 0, s>>>(a); break;
+    case kRedTop4: score_kernel<DOC, RES, L, NT, kRedTop4, false, KC><<<grid, kThr, 0, s>>>(a); break;
+    case kRedLse: score_kernel<DOC, RES, L, NT, kRedLse, false, KC><<<grid, kThr, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -845,7 +1033,8 @@ int score_rows_per_pass(int limbs, int64_t rows, int chunks) {
 
 hipError_t launch_score(const ScoreArgs& a, int doc, bool residual, int limbs, int reducer, int64_t groups,
                         hipStream_t stream) {
-  if (a.num_waves <= 0 || a.num_waves % kWavesPerGroup != 0 || a.subs <= 0 || groups <= 0)
+  if (a.num_waves <= 0 || a.subs <= 0 || groups <= 0) return hipErrorInvalidValue;
+  if (a.group_units > 0 ? a.num_waves % a.group_units != 0 : a.num_waves % kWavesPerGroup != 0)
     return hipErrorInvalidValue;
   if (a.tscale == nullptr || (residual && (a.rcodes == nullptr || a.rtscale == nullptr)))
     return hipErrorInvalidValue;

@@ -85,4 +85,61 @@ void build_score_tables(const int64_t* off, const int64_t* targets, int64_t n, i
   }
 }
 
+int64_t build_score_units(const int64_t* off, const int64_t* targets, int64_t n, int64_t workgroups,
+                          std::vector<int64_t>& info, std::vector<uint64_t>& tiles) {
+  info.clear();
+  tiles.clear();
+  workgroups = std::max<int64_t>(1, std::min(workgroups, std::max<int64_t>(1, n)));
+  auto doc_of = [&](int64_t t) { return targets ? targets[t] : t; };
+  auto tiles_of = [&](int64_t t) {
+    const int64_t d = doc_of(t);
+    return std::max<int64_t>(1, (off[d + 1] - off[d] + 15) / 16);
+  };
+  std::vector<int64_t> order((size_t)n);
+  for (int64_t t = 0; t < n; ++t) order[(size_t)t] = t;
+  std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return tiles_of(a) > tiles_of(b); });
+  using Load = std::pair<int64_t, int64_t>;  // (cost so far, list)
+  std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+  for (int64_t w = 0; w < workgroups; ++w) heap.push({0, w});
+  std::vector<std::vector<int64_t>> mine((size_t)workgroups);  // each longest first
+  for (int64_t t : order) {
+    Load l = heap.top();
+    heap.pop();
+    mine[(size_t)l.second].push_back(t);
+    heap.push({l.first + tiles_of(t) + 1, l.second});
+  }
+  std::vector<std::vector<int64_t>> units((size_t)workgroups);  // records, kScoreInfoWords each
+  int64_t most = 1;
+  for (int64_t w = 0; w < workgroups; ++w) {
+    auto& rec = units[(size_t)w];
+    int64_t tab0 = (int64_t)tiles.size(), count = 0;
+    auto close = [&]() {
+      const int64_t row[kScoreInfoWords] = {0, count, (int64_t)tiles.size() - tab0, tab0};
+      rec.insert(rec.end(), row, row + kScoreInfoWords);
+      tab0 = (int64_t)tiles.size();
+      count = 0;
+    };
+    for (int64_t t : mine[(size_t)w]) {
+      const int64_t d = doc_of(t);
+      const int64_t s = off[d], e = off[d + 1];
+      if (s == e) tiles.push_back(score_tile_entry(0, 1, true, true, t));
+      for (int64_t x = s; x < e; x += 16)
+        tiles.push_back(score_tile_entry(x, std::min<int64_t>(16, e - x), x + 16 >= e, false, t));
+      ++count;
+      if ((int64_t)tiles.size() - tab0 >= kScoreUnitMinTiles) close();
+    }
+    if (count > 0) close();
+    most = std::max<int64_t>(most, (int64_t)rec.size() / kScoreInfoWords);
+  }
+  for (auto& rec : units) {
+    while ((int64_t)rec.size() / kScoreInfoWords < most) {
+      const int64_t pad[kScoreInfoWords] = {0, 0, 0, 0};
+      rec.insert(rec.end(), pad, pad + kScoreInfoWords);
+    }
+    info.insert(info.end(), rec.begin(), rec.end());
+  }
+  if (tiles.empty()) tiles.push_back(score_tile_entry(0, 1, false, false, 0));
+  return most;
+}
+
 }  // namespace msim
