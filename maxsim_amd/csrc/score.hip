@@ -41,6 +41,11 @@ constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / kWave;
 constexpr float kLimbStep = 1.0f / 254.0f;
 constexpr float kLimbStep2 = 1.0f / 64516.0f;  // 254^-2
+// Limb accumulator starts of the biased three-limb form (score_kernel):
+// limb 1 starts at -kLimb1Bias, limb 2 at the bits of kLimb1Bias * 254 =
+// 12583160 = 2^23 + 4194552 (the float's bits 0x4B000000 + 4194552).
+constexpr int kLimb1Bias = 49540;
+constexpr int kLimb2Bias = 0x4B000000 + 4194552;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLowest = -3.402823466e+38f;
 
@@ -356,9 +361,29 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
     v4i s[L][NT];
     v4i r[RES ? L : 1][RES ? NT : 1];
   };
+  // int4 documents with three limbs and one or two 128-dim chunks: limb 1's
+  // accumulator starts at -kLimb1Bias and limb 2's at the bits of
+  // K = 254 kLimb1Bias = 12583160, in [2^23, 2^24) with room for
+  // |a2| <= 128 * 127 * 128 * KC < 2^22 on either side, so it holds the
+  // float K + a2 exactly.  The similarity s (a0 + a1 / 254 + a2 / 254^2)
+  // (s: token scale times tmul) is then
+  //   fma(W, s / 254, fma(F2, s / 254^2, add)),  W = 254 a0 + a1 - kLimb1Bias
+  // (one v_mad_i32_i24; |a0| < 2^23, |W| < 2^31), F2 the accumulator read as
+  // a float: four VALU instructions instead of five (no conversion of a2),
+  // the biases cancelling as -kLimb1Bias s / 254 + K s / 254^2 = 0.  With
+  // q1 = s / 254 and q2 = s / 254^2 rounded separately the cancellation
+  // leaves at most about 2^-23 K q2 < 2 s / 254^2 < 3.1e-5 s, and the
+  // rounding of fma(F2, q2, add) near K q2 adds 0.5 ulp of it, about 0.75 s
+  // / 254^2: against terms of s a0, |a0| in the thousands for any sizeable
+  // similarity.  `add` (-0 or a mask's -inf) joins the inner fma.
+  // (Not with the residual stream at two chunks: its registers would drop
+  // the kernel to one wave per SIMD.)
+  constexpr bool kBias2 = L == 3 && DOC == kDocInt4 && (KC == 1 || (KC == 2 && !RES));
   struct Pend {
     uint64_t e;
     float s[4], sr[4];
+    float q1[kBias2 ? 4 : 1], q2[kBias2 ? 4 : 1];
+    float r1[kBias2 && RES ? 4 : 1], r2[kBias2 && RES ? 4 : 1];
   };
   auto pend_of = [&](const Tile& t) {
     Pend q;
@@ -367,8 +392,24 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
     for (int rr = 0; rr < 4; ++rr) {
       q.s[rr] = t.s[rr];
       q.sr[rr] = RES ? t.sr[rr] : 0.0f;
+      if constexpr (kBias2) {
+        q.q1[rr] = t.s[rr] * (p.tmul * kLimbStep);
+        q.q2[rr] = t.s[rr] * (p.tmul * kLimbStep2);
+        if constexpr (RES) {
+          q.r1[rr] = t.sr[rr] * (p.rmul * kLimbStep);
+          q.r2[rr] = t.sr[rr] * (p.rmul * kLimbStep2);
+        }
+      }
     }
     return q;
+  };
+  // C operand of a limb's first MFMA of a tile.
+  v4i cbias1 = {-kLimb1Bias, -kLimb1Bias, -kLimb1Bias, -kLimb1Bias};
+  v4i cbias2 = {kLimb2Bias, kLimb2Bias, kLimb2Bias, kLimb2Bias};
+  if constexpr (kBias2) asm volatile("" : "+v"(cbias1), "+v"(cbias2));  // kept in VGPRs
+  auto cstart = [&](int l) -> v4i {
+    const v4i zero = {0, 0, 0, 0};
+    return !kBias2 || l == 0 ? zero : l == 1 ? cbias1 : cbias2;
   };
   struct Ops {
     v4i a0, a1, r0, r1;
@@ -425,6 +466,16 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
       const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
       return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
     };
+    if constexpr (kBias2) {
+      // The biased form (see Pend).
+      auto biased = [&](const v4i (&a)[L][NT], float q1, float q2, float add_) {
+        const int w = __mul24(a[0][j][rr], 254) + a[1 % L][j][rr];  // v_mad_i32_i24
+        return fmaf((float)w, q1, fmaf(__int_as_float(a[2 % L][j][rr]), q2, add_));
+      };
+      float z = biased(A.s, P.q1[rr], P.q2[rr], add);
+      if constexpr (RES) z = z + biased(A.r, P.r1[rr], P.r2[rr], -0.0f);
+      return z;
+    }
     float Y;
     if constexpr (L == 3 && DOC == kDocInt4) {
       Y = limbs3(A.s);
@@ -563,7 +614,7 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
       for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int l = 0; l < L; ++l)
-          Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][kc][0], kc == 0 ? zero : Q.s[l][j], 0, 0, 0);
+          Q.s[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[l][j][kc][0], kc == 0 ? cstart(l) : Q.s[l][j], 0, 0, 0);
 #pragma unroll
       for (int j = 0; j < NT; ++j)
 #pragma unroll
@@ -579,7 +630,7 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
         for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int l = 0; l < L; ++l)
-            Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][kc][0], kc == 0 ? zero : Q.r[l][j], 0, 0, 0);
+            Q.r[l][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(r0, bq[l][j][kc][0], kc == 0 ? cstart(l) : Q.r[l][j], 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
@@ -768,8 +819,8 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
 #pragma unroll
       for (int k = 0; k < 2 * L; ++k) {
         const int l = k % L, h = k / L;
-        A.s[l][jq] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][jq][0][h], h ? A.s[l][jq] : zero,
-                                                          0, 0, 0);
+        A.s[l][jq] = __builtin_amdgcn_mfma_i32_16x16x64_i8(h ? o.a1 : o.a0, bq[l][jq][0][h],
+                                                          h ? A.s[l][jq] : cstart(l), 0, 0, 0);
         if (epi && k < 4) z[k] = zval(A, P, jp, k, m[k]);
         __builtin_amdgcn_sched_barrier(0);
       }

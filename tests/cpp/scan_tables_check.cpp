@@ -10,6 +10,11 @@
 // documents or candidate targets (with duplicates): every target's tokens are
 // covered by its tiles in order, exactly once, its last tile flagged, an empty
 // target gets one empty tile, and every wave ends with a padding entry.
+// build_score_units (score_tables.cpp): the same coverage over the units of
+// every workgroup's list, each unit whole targets (its last tile ends one),
+// tile entries with absolute target indices, every unit but a list's last of
+// at least kScoreUnitMinTiles tiles, and every list padded to the returned
+// count with empty records at its end.
 #include <cstdio>
 #include <vector>
 #include <cstdint>
@@ -103,6 +108,56 @@ int main() {
       const int64_t d = cand ? targets[t] : t;
       if (lasts[t] != 1) { printf("BAD score lasts %d\n", t); return 1; }
       if (off[d + 1] != off[d] && next_tok[t] != off[d + 1]) { printf("BAD score cover\n"); return 1; }
+    }
+  }
+  // build_score_units
+  for (int trial = 0; trial < 200; ++trial) {
+    int n = 1 + rng() % 3000; std::vector<int64_t> off(n + 1, 0);
+    for (int d = 0; d < n; ++d) off[d + 1] = off[d] + (rng() % 5 == 0 ? 0 : rng() % (trial % 2 ? 40 : 200));
+    std::vector<int64_t> targets;
+    const bool cand = trial % 3 == 2;
+    const int nt = cand ? 1 + rng() % 500 : n;
+    for (int t = 0; t < nt && cand; ++t) targets.push_back(rng() % n);
+    const int64_t wgs = 1 + rng() % 300;
+    std::vector<int64_t> info; std::vector<uint64_t> tiles;
+    const int64_t U = msim::build_score_units(off.data(), cand ? targets.data() : nullptr, nt, wgs, info, tiles);
+    const int64_t G = std::min<int64_t>(wgs, nt);
+    if (U < 1 || (int64_t)info.size() != G * U * msim::kScoreInfoWords) { printf("BAD units size\n"); return 1; }
+    std::vector<int64_t> next_tok(nt, -1); std::vector<int> lasts(nt, 0);
+    for (int64_t g = 0; g < G; ++g) {
+      bool ended = false;
+      for (int64_t k = 0; k < U; ++k) {
+        const int64_t* r = &info[(g * U + k) * msim::kScoreInfoWords];
+        if (r[2] == 0) { ended = true; continue; }
+        const bool last_unit = k + 1 == U || info[(g * U + k + 1) * msim::kScoreInfoWords + 2] == 0;
+        if (ended || r[0] != 0 || (!last_unit && r[2] < msim::kScoreUnitMinTiles)) { printf("BAD unit\n"); return 1; }
+        int64_t ends = 0;
+        for (int64_t i = 0; i < r[2]; ++i) {
+          const uint64_t e = tiles[r[3] + i];
+          const int64_t start = (int64_t)(e & msim::kTileStartMask);
+          const int rows = (int)((e >> msim::kTileRowsShift) & 15) + 1;
+          const bool last = (e >> msim::kTileLastShift) & 1, empty = (e >> msim::kTileEmptyShift) & 1;
+          const int64_t t = (int64_t)(e >> msim::kTileLocalShift);
+          if (t < 0 || t >= nt) { printf("BAD unit target\n"); return 1; }
+          const int64_t d = cand ? targets[t] : t;
+          if (empty) {
+            if (off[d + 1] != off[d] || !last) { printf("BAD unit empty\n"); return 1; }
+          } else {
+            const int64_t expect = next_tok[t] < 0 ? off[d] : next_tok[t];
+            if (start != expect || start + rows > off[d + 1]) { printf("BAD unit tile\n"); return 1; }
+            next_tok[t] = start + rows;
+            if (last != (start + rows == off[d + 1])) { printf("BAD unit last\n"); return 1; }
+          }
+          lasts[t] += last ? 1 : 0;
+          ends += last ? 1 : 0;
+          if (i + 1 == r[2] && !last) { printf("BAD unit splits a target\n"); return 1; }
+        }
+        if (ends != r[1]) { printf("BAD unit count\n"); return 1; }
+      }
+    }
+    for (int t = 0; t < nt; ++t) {
+      const int64_t d = cand ? targets[t] : t;
+      if (lasts[t] != 1 || (off[d + 1] != off[d] && next_tok[t] != off[d + 1])) { printf("BAD unit cover %d\n", t); return 1; }
     }
   }
   printf("ok\n");

@@ -89,6 +89,34 @@ def test_int4_reducers_ragged_many_rows(gpu, oracle, reducer):
     _close(got, exp)
 
 
+@pytest.mark.parametrize("reducer", REDUCERS)
+@pytest.mark.parametrize("corpus", ["tiny_docs", "three_docs"])
+def test_int4_work_units(gpu, oracle, reducer, corpus):
+    """The row-block pipeline's work units (fp32 queries of more than 32
+    rows over the whole corpus): 3000 documents of 0..20 tokens, a fifth
+    empty (units of several documents each), or three documents (fewer
+    units than the workgroup's eight waves)."""
+    print(f"case: work units corpus={corpus} reducer={reducer}", flush=True)
+    if corpus == "tiny_docs":
+        rng = np.random.default_rng(17)
+        lengths = rng.integers(0, 21, size=3000)
+        lengths[rng.random(3000) < 0.2] = 0
+        offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+        docs = rng.standard_normal((int(offsets[-1]), 128)).astype(np.float32)
+    else:
+        docs, offsets = ragged_fixture(3, 18, lo=1, hi=90, empty=None)
+    rng = np.random.default_rng(19)
+    query = rng.standard_normal((2, 40, 128)).astype(np.float32)
+    weights = rng.uniform(0.5, 1.5, size=(2, 40)).astype(np.float32)
+    packed, h = _int4_handle(docs, offsets, "token")
+    w = weights if reducer == "weighted_maxsim" else None
+    got = h.score_batch(query, reducer=reducer, query_weights=w, temperature=0.7)
+    exp = oracle.int4_fp32_scores(query, packed.values, offsets, token_scale=packed.token_scale, reducer=reducer,
+                                  weights=w, temperature=0.7)
+    _close(got, exp)
+    assert np.all(got[:, np.diff(offsets) == 0] == 0.0)
+
+
 @pytest.mark.parametrize("shape", ["1d", "1xQ", "BxQ"])
 def test_weight_shapes(gpu, oracle, shape):
     docs, offsets, query, weights, _ = _reducer_fixture()
