@@ -47,6 +47,7 @@ constexpr float kLimbStep2 = 1.0f / 64516.0f;  // 254^-2
 constexpr int kLimb1Bias = 49540;
 constexpr int kLimb2Bias = 0x4B000000 + 4194552;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLowest = -3.402823466e+38f;
 
 template <int RED>
@@ -110,39 +111,42 @@ struct ReducerState<kRedTop2> : TopState<2> {};
 template <>
 struct ReducerState<kRedTop4> : TopState<4> {};
 
-// kRedLse: online log-sum-exp in base 2 over x = z * (colmul * doc_scale):
-// m = running maximum (starts at the lowest finite float so that masked
-// -inf values never form inf - inf), s = sum 2^((x - m) * log2(e) / tau).
-// Every exponent is <= 0 and the maximum's term is 1, so v_exp_f32 itself
-// serves (exp2f adds a rescaling path for results below 2^-126, which are
-// negligible next to that 1).
+// kRedLse: online log-sum-exp in base 2 over u = z * k with k = colmul *
+// doc_scale * log2(e) / tau, i.e. u = x log2(e) / tau for the scaled
+// similarity x = z * colmul * doc_scale: m = running maximum of u (starts at
+// the lowest finite float so that masked -inf values never form inf - inf),
+// s = sum 2^(u - m).  Every exponent is <= 0 and the maximum's term is 1, so
+// v_exp_f32 itself serves (exp2f adds a rescaling path for results below
+// 2^-126, which are negligible next to that 1).  The score, max x + tau ln
+// sum e^((x - max x) / tau), is then (m + log2 s) * tau * ln 2.  (Folding
+// log2(e) / tau into k saves a multiply per similarity.)
 __device__ __forceinline__ float exp2_nonpos(float x) { return __builtin_amdgcn_exp2f(x); }
 template <>
 struct ReducerState<kRedLse> {
-  float m, s, k;  // k = colmul * doc_scale of the current target
+  float m, s, k;  // k = colmul * doc_scale * log2(e) / tau for the current target
   __device__ void init() {
     m = kLowest;
     s = 0.0f;
   }
-  __device__ void add4(const float (&z)[4], float k2) {
-    float x[4];
+  __device__ void add4(const float (&z)[4], float) {
+    float u[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = z[r] * k;
-    const float mn = fmaxf(m, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-    float acc = s * exp2_nonpos((m - mn) * k2);
+    for (int r = 0; r < 4; ++r) u[r] = z[r] * k;
+    const float mn = max3_op(max3_op(m, u[0], u[1]), u[2], u[3]);
+    float acc = s * exp2_nonpos(m - mn);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc += exp2_nonpos((x[r] - mn) * k2);
+    for (int r = 0; r < 4; ++r) acc += exp2_nonpos(u[r] - mn);
     s = acc;
     m = mn;
   }
-  __device__ void merge_xor(int mask, float k2) {
+  __device__ void merge_xor(int mask, float) {
     const float mo = __shfl_xor(m, mask), so = __shfl_xor(s, mask);
     const float mn = fmaxf(m, mo);
-    s = s * exp2_nonpos((m - mn) * k2) + so * exp2_nonpos((mo - mn) * k2);
+    s = s * exp2_nonpos(m - mn) + so * exp2_nonpos(mo - mn);
     m = mn;
   }
   __device__ float finish(int len, float, float temperature, float, float) const {
-    return len == 0 ? 0.0f : m + temperature * logf(s);
+    return len == 0 ? 0.0f : (m + log2f(s)) * (temperature * kLn2);
   }
 };
 
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
       dscale = doc_scale ? doc_scale[doc] : p.scale;
       if constexpr (RED == kRedLse) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale;
+        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale * k2;
       }
     }
     return ((e >> kTileEmptyShift) & 1) ? 0 : (int)((e >> kTileRowsShift) & 15) + 1;
@@ -720,7 +724,7 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
       dscale = doc_scale ? doc_scale[doc] : p.scale;
       if constexpr (RED == kRedLse) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale;
+        for (int j = 0; j < NT; ++j) st[j].k = colmul[j] * dscale * k2;
       }
     }
     auto fetch = [&](int i, Tile& t) __attribute__((always_inline)) {
