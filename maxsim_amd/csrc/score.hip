@@ -463,9 +463,10 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
   auto zval = [&](const Acc& A, const Pend& P, int j, int rr, float add) __attribute__((always_inline)) {
     // Limb dots combined smallest first; sign documents recover the +-1 dot
     // as 2 (q . bits) - sum(q).
-    // int4 documents with three limbs: the two small limbs first as one
-    // exact integer, 254 a1 + a2 (|a| <= 128 * 127 * 128 KC < 2^23 for
-    // KC <= 4, so the 24-bit multiply and the int32 sum are exact).
+    // int4 documents with three limbs, where the biased form does not apply
+    // (four chunks, or the residual stream at two): the two small limbs
+    // first as one exact integer, 254 a1 + a2 (|a| <= 128 * 127 * 128 KC <
+    // 2^23 for KC <= 4, so the 24-bit multiply and the int32 sum are exact).
     auto limbs3 = [&](const v4i (&a)[L][NT]) {
       const int z12 = __mul24(a[1 % L][j][rr], 254) + a[2 % L][j][rr];  // v_mad_i32_i24
       return fmaf((float)z12, kLimbStep2, (float)a[0][j][rr]);
@@ -776,6 +777,7 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
     // (the older wave issues first); taking units as they go, both finish
     // with the workgroup's list.
     constexpr int kRing = 4;
+    static_assert(kScoreUnitMinTiles >= kRing - 1, "units cover the tiles loaded ahead");
     const bool units = p.group_units > 0;
     const auto unit_info = as_constant(p.wave_info) + grp * p.info_grp_stride +
                            (int64_t)blockIdx.x * p.group_units * kScoreInfoWords;
