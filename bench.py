@@ -55,6 +55,16 @@ MFMA_FP4_PEAK_TOPS = 10100.0  # MI355X dense fp4 MFMA
 MIX_NS_PER_MFMA = 11.43
 RAMP_US = 2.4
 TAIL_US = 4.8
+# Config 3's MaxSim score launch, the same way: its loop issues 24 MFMAs per
+# 16-token tile and pass (three limbs, four row blocks) with about five other
+# VALU instructions each (profiles/score_kernel_config3_sq_counters.md: 4.95),
+# a mix the rate tests put between mfma_fma4 (12.79 ns per MFMA) and
+# mfma_fma6 (15.61 ns): 14.2 ns.  The first tile lands at 2.0 us (median
+# wave, per-wave stamps) and the last wave ends its loop about 1 us before
+# the launch ends.
+MIX3_NS_PER_MFMA = 14.2
+RAMP3_US = 2.0
+TAIL3_US = 1.0
 
 
 def parse_args():
@@ -658,6 +668,18 @@ def bench_config3(args):
             "fp32_equivalent_TFLOPs": ops / (ms * 1e-3) / 1e12, "fp32_vector_peak_TFLOPs": FP32_PEAK_TFLOPS,
             "note": "step time (scan + top-10); int8 ops = 3 limbs x 2 B Q T 128"}
     roof["frac"] = roof["achieved"] / roof["peak"]
+    # The MaxSim launch's issue bound (see MIX3_NS_PER_MFMA): two 64-row passes
+    # over every tile, spread over the chip's SIMDs.
+    simds = torch.cuda.get_device_properties(0).multi_processor_count * 4
+    passes = (b * q + 63) // 64
+    tiles_per_simd = passes * scan_tiles(packed.doc_offsets) / simds
+    bound_us = RAMP3_US + tiles_per_simd * 24 * MIX3_NS_PER_MFMA * 1e-3 + TAIL3_US
+    roof["maxsim_achievable_bound"] = {
+        "kernel_us": bound_us, "frac": 3 * ops / (bound_us * 1e-6) / 1e12 / MFMA_INT8_PEAK_TOPS,
+        "tiles_per_simd": tiles_per_simd,
+        "basis": "ramp %.1f us + tiles per SIMD x 24 MFMAs x %.1f ns (an MFMA and about five VALU instructions, "
+                 "two waves per SIMD, rate tests) + tail %.1f us; against the MaxSim launch's measured "
+                 "score_kernel_ms" % (RAMP3_US, MIX3_NS_PER_MFMA, TAIL3_US)}
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
