@@ -604,10 +604,9 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
   };
   // All MFMAs of a tile: the first stream's halves, chunk by chunk, then the
   // residual's (its operands unpacked only then, so fewer registers are
-  // live).  Chunk 0's first half starts from zero; every later MFMA adds to
-  // the same accumulators.
+  // live).  Chunk 0's first half starts from the limb's start value
+  // (cstart); every later MFMA adds to the same accumulators.
   auto issue = [&](Acc& Q, const Tile& tq) __attribute__((always_inline)) {
-    const v4i zero = {0, 0, 0, 0};
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       v4i a0, a1;
@@ -820,7 +819,6 @@ __global__ __launch_bounds__(kWave * score_group_waves(NT, L, RES, KC), NT == 8 
     };
     auto step = [&](const Ops& o, int jq, bool epi, const Pend& P, const float (&m)[4], int jp)
                     __attribute__((always_inline)) {
-      const v4i zero = {0, 0, 0, 0};
       float z[4];
 #pragma unroll
       for (int k = 0; k < 2 * L; ++k) {
