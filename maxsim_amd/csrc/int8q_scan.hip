@@ -249,11 +249,17 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // t + c for dims [32g, 32g + 32) and the (pre-divided by 16) scale of
   // token t + c; a lane then reads the four scales of its accumulator rows
   // 4g..4g+3 as one 16-byte LDS read.  The tile's byte offset is the loads'
-  // scalar offset, the lane's part a constant VGPR.  Every step issues
-  // exactly kOps loads, so slot i is complete once vmcnt <= (kPrefetch - 1) *
-  // kOps.
+  // scalar offset, the lane's part a constant VGPR.  Tile x goes to ring
+  // slot x % kPrefetch.  The wave starts with kStartTiles tiles in flight
+  // and fills the ring over its first kRampStages steps, three tiles each
+  // (every wave asking for its whole ring at the start takes about 1.8 us
+  // to issue, the first tile then lands 0.4 us later); from then on every
+  // step issues exactly kOps loads, so the tile read next is complete once
+  // vmcnt <= (kPrefetch - 1) * kOps.
   constexpr int kOps = kTS ? 2 : 1;
   constexpr int kRingWait = (kPrefetch - 1) * kOps;
+  constexpr int kStartTiles = 2, kRampStages = 3;
+  static_assert(kStartTiles + 2 * kRampStages == kPrefetch, "after the ramp the ring runs kPrefetch tiles ahead");
   const uint32_t voff_codes = kSign ? 16u * (uint32_t)c + 4u * (uint32_t)g : 64u * (uint32_t)c + 16u * (uint32_t)g;
   const uint32_t voff_scales = 4u * (uint32_t)c;
   auto load_tile = [&](int slot_, uint32_t t) {
@@ -263,11 +269,17 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     if (kTS) lds_load_b32_so(rs, voff_scales, tu * 4u, ring_scales + slot_ * kWave * 4);
   };
 #pragma unroll
-  for (int s = 0; s < kPrefetch; ++s) load_tile(s, (uint32_t)tt[s]);
+  for (int s = 0; s < kStartTiles; ++s) load_tile(s, (uint32_t)tt[s]);
+  // First tokens of the ramp's tiles kStartTiles .. kStartTiles + 3
+  // kRampStages - 1 (the table has at least kScanMinStride entries per wave).
+  static_assert(kStartTiles + 3 * kRampStages <= kScanMinStride, "ramp entries inside the wave's table row");
+  uint32_t ramp_tok[3 * kRampStages];
+#pragma unroll
+  for (int x = 0; x < 3 * kRampStages; ++x) ramp_tok[x] = (uint32_t)tt[kStartTiles + x];
 
-  // The query tiles (and scales) are complete once at most kPrefetch * kOps
-  // loads are outstanding; the barrier publishes all four quarters.
-  vm_wait_lds<kPrefetch * kOps>();
+  // The query tiles (and scales) are complete once at most kStartTiles *
+  // kOps loads are outstanding; the barrier publishes all four quarters.
+  vm_wait_lds<kStartTiles * kOps>();
   __builtin_amdgcn_s_barrier();
   if (fused) tag = (uint32_t)wave_uniform((int)__float_as_uint(rowmax[0])) + 1u;
   // Sign documents (A bytes 0 / 2 from the sign bits): the first MFMA of
@@ -471,20 +483,31 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     uint32_t mhi_p;      // and its table entry (high half)
     uint64_t meta = tt[0], iss = tt[kPrefetch];
     int slot = 0;
-    vm_wait_lds<kRingWait>();
+    vm_wait_lds<(kStartTiles - 1) * kOps>();
     auto read_codes = [&](int sl) -> v4u {
       if (kSign) return (v4u){reinterpret_cast<const uint32_t*>(&s_codes[wave][sl][0])[lane], 0u, 0u, 0u};
       return s_codes[wave][sl][lane];
     };
     v4u w = read_codes(0);
     v4u sv = kTS ? *reinterpret_cast<const v4u*>(&s_scales[wave][0][0] + 4 * g) : (v4u){0u, 0u, 0u, 0u};
-    // Read-ahead after tile `slot` left the ring for registers.
-    auto advance = [&](int i_next) {
+    // Read-ahead after tile `slot` left the ring for registers.  Stage K
+    // (1..kRampStages, the advances to tiles 1..kRampStages) issues tiles
+    // 3K - 1 .. 3K + 1 into their slots, none of them holding a tile still
+    // to be read, and then 2K + 1 tiles past tile K are in flight; stage 0
+    // refills the slot just left with tile i_next - 1 + kPrefetch.
+    auto advance = [&](int i_next, auto stage) {
+      constexpr int K = decltype(stage)::value;
       lds_read_done(w, sv);
-      load_tile(slot, (uint32_t)iss);
+      if constexpr (K == 0) {
+        load_tile(slot, (uint32_t)iss);
+      } else {
+#pragma unroll
+        for (int x = 3 * K - 1; x <= 3 * K + 1; ++x) load_tile(x % kPrefetch, ramp_tok[x - kStartTiles]);
+      }
       const uint64_t meta_n = tt[i_next], iss_n = tt[i_next + kPrefetch];
       slot = slot + 1 == kPrefetch ? 0 : slot + 1;
-      vm_wait_lds<kRingWait>();
+      if constexpr (K == 0) vm_wait_lds<kRingWait>();
+      else vm_wait_lds<(2 * K + 1) * kOps>();
       w = read_codes(slot);
       if (kTS) sv = *reinterpret_cast<const v4u*>(&s_scales[wave][slot][0] + 4 * g);
       meta = meta_n;
@@ -495,15 +518,15 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       mhi_p = (uint32_t)(meta >> 32);
       const v4i cinit = prep(mhi_p, sv, epi_p);
       const v4u w_q = w;
-      advance(1);
+      advance(1, std::integral_constant<int, 1>{});
       issue_and_finish(acc_a, w_q, cinit, acc_b, epi_p, false);
     }
-    auto step = [&](int i, v4i (&acc_p)[NT], v4i (&acc_q)[NT]) {
+    auto step = [&](int i, v4i (&acc_p)[NT], v4i (&acc_q)[NT], auto stage) {
       const uint32_t mhi_q = (uint32_t)(meta >> 32);
       TileEpi epi_q;
       const v4i cinit = prep(mhi_q, sv, epi_q);
       const v4u w_q = w;
-      advance(i + 2);
+      advance(i + 2, stage);
       issue_and_finish(acc_q, w_q, cinit, acc_p, epi_p, true);
       if ((mhi_p >> 5) & 1u) finish((int)(mhi_p >> 8));
       mhi_p = mhi_q;
@@ -514,13 +537,23 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       epilogue(acc_p, epi_p);
       finish((int)(mhi_p >> 8));  // the last tile always ends a document
     };
+    using Ramp2 = std::integral_constant<int, 2>;
+    using Ramp3 = std::integral_constant<int, 3>;
+    using Steady = std::integral_constant<int, 0>;
+    static_assert(kRampStages == 3, "two ramp stages after the prologue's");
     int i = 0;
+    if (ntiles > 2) {
+      step(0, acc_a, acc_b, Ramp2{});
+      step(1, acc_b, acc_a, Ramp3{});
+      i = 2;
+    }
     for (; i + 2 < ntiles; i += 2) {
-      step(i, acc_a, acc_b);
-      step(i + 1, acc_b, acc_a);
+      step(i, acc_a, acc_b, Steady{});
+      step(i + 1, acc_b, acc_a, Steady{});
     }
     if (i + 1 < ntiles) {
-      step(i, acc_a, acc_b);
+      if (i == 0) step(0, acc_a, acc_b, Ramp2{});  // two tiles: the ramp's second stage reads tile 2
+      else step(i, acc_a, acc_b, Steady{});
       last(acc_b);
     } else {
       last(acc_a);

@@ -73,6 +73,7 @@ constexpr int kScanWavesPerGroup = 4;
 #define MSIM_SCAN_PREFETCH 8
 #endif
 constexpr int kScanPrefetch = MSIM_SCAN_PREFETCH;  // ring depth: tiles in flight per wave
+constexpr int64_t kScanMinStride = 16;             // tile-table entries per wave at least
 #ifndef MSIM_SCAN_WAVES_PER_CU
 #define MSIM_SCAN_WAVES_PER_CU 8
 #endif

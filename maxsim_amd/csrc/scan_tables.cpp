@@ -129,11 +129,13 @@ void build_scan_tables(const int64_t* off, int64_t n, int64_t waves, bool contig
   }
   // Every wave's entries at a fixed stride (a multiple of 8 entries, 64 B),
   // so a wave finds them from its index alone, without reading its row of
-  // `info` first; the rest of a slot is padding.
+  // `info` first; the rest of a slot is padding.  At least kScanMinStride
+  // entries: a wave reads its first 11 entries while it fills its ring,
+  // whatever its tile count.
   num_waves = (int64_t)info.size() / kWaveInfoWords;
   int64_t longest = 0;
   for (int64_t w = 0; w < num_waves; ++w) longest = std::max<int64_t>(longest, info[w * kWaveInfoWords + 4]);
-  stride = ((longest + kScanPrefetch + 1 + 7) / 8) * 8;
+  stride = std::max<int64_t>(kScanMinStride, ((longest + kScanPrefetch + 1 + 7) / 8) * 8);
   table.assign((size_t)(num_waves * stride), kScanPadEntry);
   // Positions in wave order: wave w's documents take [pos0, pos0 + all_docs).
   std::vector<int64_t> block_pos;

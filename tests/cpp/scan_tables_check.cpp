@@ -34,8 +34,11 @@ int main() {
       for (int64_t w = 0; w < nw; ++w) total_empty += info[w * 8 + 6];
       const int64_t* block_pos = &info[nw * 8 + total_empty];
       if ((int64_t)info.size() != nw * 8 + total_empty + nw / 4 + 1 || block_pos[nw / 4] != n) { printf("BAD block_pos size\n"); return 1; }
+      // The kernel reads entries 0 .. max(ntiles + prefetch, 10) of its row.
+      if (stride < msim::kScanMinStride || stride % 8 != 0) { printf("BAD stride\n"); return 1; }
       for (int64_t w = 0; w < nw; ++w) {
         const int64_t* r = &info[w * 8];
+        if (r[4] + msim::kScanPrefetch + 1 > stride) { printf("BAD stride for w%ld\n", (long)w); return 1; }
         if (w % 4 == 0 && block_pos[w / 4] != r[5]) { printf("BAD block_pos\n"); return 1; }
         int64_t next = r[5];
         auto place = [&](int64_t doc) -> bool {
