@@ -50,10 +50,10 @@ MFMA_FP4_PEAK_TOPS = 10100.0  # MI355X dense fp4 MFMA
 # three VALU instructions with two waves per SIMD (bench.py --rates,
 # mfma_fma3: 11.43 ns per MFMA), plus the time until a wave's first tile
 # lands (median wave, per-wave s_memrealtime stamps of a timing copy of the
-# kernel: 2.4 us) and the tail from the last wave's loop end to the end of
+# kernel: 2.1 us) and the tail from the last wave's loop end to the end of
 # the selection (the same stamps: 4.8 us).
 MIX_NS_PER_MFMA = 11.43
-RAMP_US = 2.4
+RAMP_US = 2.1
 TAIL_US = 4.8
 # Config 3's MaxSim score launch, the same way: its loop issues 24 MFMAs per
 # 16-token tile and pass (three limbs, four row blocks) with about five other
