@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // Global loads, all with an LDS destination (untracked by the compiler,
   // waited for explicitly), in this order: the workgroup's query tiles (each
   // wave a quarter of the 1 KiB half-tiles, lane order), this wave's query
-  // scales, the first kPrefetch tiles.
+  // scales, the wave's first kStartTiles tiles.
   {
     const v4i rqp = make_rsrc_words(qpack, (uint32_t)(NT * 2048));
     const uint32_t q_lds = wave_uniform((int)lds_address(s_query));

@@ -160,6 +160,33 @@ def test_int8q_scan_partitions_agree_with_oracle(gpu, oracle, scan_partition, le
         np.testing.assert_array_equal(top_s, ref_s)
 
 
+def test_int8q_scan_ring_fill_short_waves(gpu, oracle):
+    """One document per wave (docs_per_wave 1) with 1 to 14 tiles each: a
+    wave starts with two ring tiles and fills the ring over its first three
+    steps, with special cases for one, two and three tiles; scores and the
+    fused top-k bit-exact vs the oracle."""
+    from maxsim_amd import _maxsim_hip
+
+    base = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 64, 65, 80, 96, 112, 128, 144, 160, 200, 224]
+    lengths = np.array(base * 16, np.int64)  # 320 documents
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    rng = np.random.default_rng(11)
+    docs = rng.standard_normal((int(offsets[-1]), 128)).astype(np.float32)
+    packed = pack_int4_symmetric(docs, offsets, scale_granularity="token")
+    query = rng.standard_normal((4, 32, 128)).astype(np.float32)
+    expected = _scores(oracle, packed, query)
+    ref_s, ref_i = oracle.topk(expected, 10)
+    _maxsim_hip.set_docs_per_wave(1)
+    try:
+        device = int4_to_device(packed)
+        np.testing.assert_array_equal(device.data.maxsim_batch_int8q(query), expected)
+        top_s, top_i = device.data.topk_batch_int8q(query, 10)
+        np.testing.assert_array_equal(top_i, ref_i)
+        np.testing.assert_array_equal(top_s, ref_s)
+    finally:
+        _maxsim_hip.set_docs_per_wave(0)
+
+
 @pytest.mark.parametrize("long_len", [4000, 16])
 def test_int8q_scan_one_long_document(gpu, oracle, scan_partition, long_len):
     """One document far longer than the rest (a wave with thousands of tiles,
