@@ -621,13 +621,17 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
     }
     // Poll gently while many workgroups are still scanning (the polls take
     // issue slots from the scan waves sharing this CU), then closely, and
-    // compute T ahead when the current records changed it may.
+    // compute T ahead when the current records changed it may.  A poll
+    // takes 1-2 us to return while the scan streams, and the last third of
+    // the records lands within the last 1.5 us, so even the gentle pause is
+    // short (8 x 64 clocks; 32 x 64 left the last poll before the end
+    // seeing 100-250 stale records and cost 0.3 us per launch).
     const int nstale = __popcll(stale_lanes);
     uint32_t lf = 0;
 #pragma unroll
     for (int j = 0; j < kTailBlocksPerLane; ++j) lf = max(lf, key_current(w0[j]) ? (uint32_t)(w0[j] >> 32) : 0u);
     const bool ahead = nstale <= 32 && (t_ahead == 0 || __ballot(lf != lmax_ahead) != 0);
-    if (nstale > 32) __builtin_amdgcn_s_sleep(32);
+    if (nstale > 32) __builtin_amdgcn_s_sleep(8);
     else if (!ahead && nstale > 4) __builtin_amdgcn_s_sleep(8);
     else if (!ahead) __builtin_amdgcn_s_sleep(1);
     issue_poll();
