@@ -136,6 +136,20 @@ struct TileEpi {
   float a[4], c[4];
 };
 
+// A dispatch's identity, as the fused selection's give-up mark stores it:
+// its packet index in its queue (the dispatch id, + 1 so that a zeroed mark
+// names no dispatch) and the queue's address.
+struct LaunchMark {
+  uint32_t w[4];
+};
+// The dispatch id has no clang builtin: the LLVM intrinsic by name.
+extern "C" __device__ uint64_t msim_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+__device__ __forceinline__ LaunchMark launch_mark() {
+  const uint64_t d = msim_dispatch_id() + 1u;
+  const uint64_t q = reinterpret_cast<uint64_t>(__builtin_amdgcn_queue_ptr());
+  return {{(uint32_t)d, (uint32_t)(d >> 32), (uint32_t)q, (uint32_t)(q >> 32)}};
+}
+
 // Bits of 2^23 as an int32: the C operand of a kScanEpiFma tile's first MFMAs.
 constexpr int kMagic = 0x4B000000;
 constexpr int kMaskedAcc = -(1 << 30);  // C operand of masked rows (|16 * dot| < 2^21)
@@ -221,9 +235,11 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
     const uint32_t qs_lds = wave_uniform((int)lds_address(qs));
     lds_load_b32(rq, 4u * (uint32_t)lane, qs_lds);
     lds_load_b32(rq, 4u * (uint32_t)(lane + kWave), qs_lds + 4 * kWave);
-    // Fused: the launch counter into lane 0's word of the row-maxima buffer
-    // (the other lanes read past the 4-byte range: 0).
-    if (fused) lds_load_b32(make_rsrc_words(p.epoch, 4u), 4u * (uint32_t)lane, wave_uniform((int)lds_address(rowmax)));
+    // Fused: the launch counter and the give-up mark (words 0 .. 5 of
+    // epoch) into words 0 .. 5 of the row-maxima buffer; the other lanes
+    // read past the 24-byte range: 0.  One load instruction over one cache
+    // line: the words come from one snapshot of the line.
+    if (fused) lds_load_b32(make_rsrc_words(p.epoch, 24u), 4u * (uint32_t)lane, wave_uniform((int)lds_address(rowmax)));
     // Sign documents: the query rows' code sums into the row-maxima buffer.
     if (kSign) {
       const v4i rsum = make_rsrc_words(p.qsum, (uint32_t)(16 * NT * 4));
@@ -281,7 +297,17 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   // kOps loads are outstanding; the barrier publishes all four quarters.
   vm_wait_lds<kStartTiles * kOps>();
   __builtin_amdgcn_s_barrier();
-  if (fused) tag = (uint32_t)wave_uniform((int)__float_as_uint(rowmax[0])) + 1u;
+  if (fused) {
+    // The launch's tag is the counter + 1, unless the give-up mark names this
+    // dispatch: then this workgroup started after its own launch's selection
+    // gave up and published the counter, and it keeps that launch's tag (its
+    // entries must not carry the next launch's tag).
+    const LaunchMark m = launch_mark();
+    bool late = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) late = late && __float_as_uint(rowmax[2 + i]) == m.w[i];
+    tag = (uint32_t)wave_uniform((int)(__float_as_uint(rowmax[0]) + (late ? 0u : 1u)));
+  }
   // Sign documents (A bytes 0 / 2 from the sign bits): the first MFMA of
   // query tile j starts at 2^23 - sum(q8) in column c, so the accumulator
   // holds 2^23 + (2 (q8 . bits) - sum(q8)) = 2^23 + q8 . signs.
@@ -618,13 +644,30 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
   if (blockIdx.x != 0) return;
   // Wave w selects batch rows w, w + 4, ... in its tile ring's LDS.
   uint64_t* lds = reinterpret_cast<uint64_t*>(&s_codes[wave][0][0]);
-  for (int b = wave; b < p.batch; b += kScanWaves)
-    tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_rec + (int64_t)b * 3 * kScanTailBlocks, (int)gridDim.x,
-              (int)p.num_docs, p.topk_k, p.tail_cap, tag, lds, bs, blen, p.top_scores + (int64_t)b * p.topk_k,
-              p.top_ids + (int64_t)b * p.topk_k, p.tail_wait_ticks, p.epoch + 1);
-  // Every workgroup read the counter at its start, before its block maxima
-  // that the selection waited for: the next launch's tag can be published.
-  if (threadIdx.x == 0) __hip_atomic_store(p.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  bool row0_selected = true;
+  for (int b = wave; b < p.batch; b += kScanWaves) {
+    const bool selected =
+        tail_topk(p.tail_keys + (int64_t)b * kScanTailRow, p.tail_rec + (int64_t)b * 3 * kScanTailBlocks,
+                  (int)gridDim.x, (int)p.num_docs, p.topk_k, p.tail_cap, tag, lds, bs, blen,
+                  p.top_scores + (int64_t)b * p.topk_k, p.top_ids + (int64_t)b * p.topk_k, p.tail_wait_ticks,
+                  p.epoch + 1);
+    if (b == 0) row0_selected = selected;
+  }
+  if (threadIdx.x == 0) {
+    if (row0_selected) {
+      // Every workgroup wrote its row-0 record, so every one read the
+      // counter at its start: the next launch's tag can be published.
+      __hip_atomic_store(p.epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      // Workgroups of this launch may not have started yet: the mark names
+      // this dispatch, then (release) the counter.  A workgroup that reads
+      // both keeps this launch's tag.
+      const LaunchMark m = launch_mark();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) __hip_atomic_store(p.epoch + 2 + i, m.w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.epoch, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 template <int EPI, bool kTail, bool kSign>

@@ -109,7 +109,9 @@ struct ScanArgs {
   // row to tail_rec [batch, 3, kScanTailBlocks] (its two largest keys, the
   // third one's score key); workgroup 0 waits until its reads carry the tag,
   // selects the top-k of every batch row into top_scores / top_ids [batch,
-  // topk_k] and stores the tag to *epoch.  tail_keys and tail_rec hold no
+  // topk_k] and stores the tag to *epoch (after a give-up of row 0, first
+  // the dispatch's identity to epoch[2..5]: a workgroup of that dispatch
+  // that starts later keeps the launch's tag).  tail_keys and tail_rec hold no
   // entry with a later launch's tag (zero them when allocated).  block_pos
   // [num_waves / 4 + 1] holds each workgroup's first position (then num_docs).
   // A selection that waits longer than tail_wait_ticks (s_memrealtime ticks,
@@ -118,7 +120,7 @@ struct ScanArgs {
   int32_t topk_k;
   int32_t tail_cap;             // 0 forces the selection's k-round path
   int64_t num_docs;
-  uint32_t* epoch;              // [0]: launch counter, [1]: selections given up
+  uint32_t* epoch;              // [0]: launch counter, [1]: selections given up, [2..5]: give-up mark (zeroed)
   uint64_t tail_wait_ticks;
   float* top_scores;
   int64_t* top_ids;

@@ -517,7 +517,8 @@ __device__ __forceinline__ void tail_block_ranges(const int64_t* bpos, int nbloc
 // then (a call would save the callee-saved registers it uses to scratch).
 // `lds_arg`: wave-private LDS of kTailLdsBytes.  1 <= k <= min(n, 64),
 // n <= kTailMaxDocs, nblocks <= kTailBlocks; bs / len from tail_block_ranges.
-__device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64_t* rec_arg, int nblocks_arg,
+// Returns false when it gave up (the row holds id -1 / NaN).
+__device__ __forceinline__ bool tail_topk(const uint64_t* keys_arg, const uint64_t* rec_arg, int nblocks_arg,
                                           int n_arg, int k_arg, int cap_arg, uint32_t tag_arg, uint64_t* lds_arg,
                                           const int (&bs)[kTailBlocksPerLane], const int (&len)[kTailBlocksPerLane],
                                           float* out_s_arg, int64_t* out_i_arg, uint64_t wait_ticks,
@@ -547,7 +548,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
   };
   if (wait_ticks == 0) {
     give_up();
-    return;
+    return false;
   }
   auto rank_below = [&](uint64_t mask) -> int {  // set bits of mask below this lane
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
@@ -617,7 +618,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
     if (stale_lanes == 0) break;
     if (expired()) {
       give_up();
-      return;
+      return false;
     }
     // Poll gently while many workgroups are still scanning (the polls take
     // issue slots from the scan waves sharing this CU), then closely, and
@@ -714,7 +715,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
         if (__ballot(st != 0) == 0) break;
         if (expired()) {
           give_up();
-          return;
+          return false;
         }
         __builtin_amdgcn_s_sleep(1);
       }
@@ -744,7 +745,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
       if (i < ncand && r < k) tail_write(y, out_s + r, out_i + r);
     }
     wave_sync_lds();
-    return;
+    return true;
   }
   // Fallback: wait until every key of the row carries the tag, then k
   // rounds over the row (read again each round): the largest full key below
@@ -761,7 +762,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
     if (__ballot(stale) == 0) break;
     if (expired()) {
       give_up();
-      return;
+      return false;
     }
     __builtin_amdgcn_s_sleep(1);
   }
@@ -779,6 +780,7 @@ __device__ __forceinline__ void tail_topk(const uint64_t* keys_arg, const uint64
     if (lane == 0) tail_write(top, out_s + r, out_i + r);
     prev = top;
   }
+  return true;
 }
 
 }  // namespace msim

@@ -7,7 +7,9 @@ ends through its own code path (no wait is cut short on the device).  The
 synchronous calls and the SDK must then raise instead of returning id -1,
 the device-resident form must leave the documented sentinel (id -1, NaN),
 and the handle's give-up counter must count it.  With the default budget
-restored, the next search must be exact again.
+restored, the next search must be exact again: with the batch rows in
+another order, so that entries left by the launch that gave up (other
+scores in every row) cannot pass for the next launch's.
 """
 import numpy as np
 import pytest
@@ -64,15 +66,21 @@ def test_given_up_selection_raises_and_counts(gpu, oracle, wait_ticks):
 
     # Default budget again: exact results, no further give-ups.
     wait_ticks(DEFAULT_TICKS)
-    got_s, got_i = handle.topk_batch_int8q(query, 10)
-    exp = oracle.int4_int8q_scores(query, packed.values, packed.doc_offsets, token_scale=packed.token_scale)
+    rquery = np.ascontiguousarray(query[::-1])
+    got_s, got_i = handle.topk_batch_int8q(rquery, 10)
+    exp = oracle.int4_int8q_scores(rquery, packed.values, packed.doc_offsets, token_scale=packed.token_scale)
     ref_s, ref_i = oracle.topk(exp, 10)
     np.testing.assert_array_equal(got_i, ref_i)
     np.testing.assert_array_equal(got_s.view(np.uint32), ref_s.view(np.uint32))
+    # The device-resident form after its own give-up, rows reversed again.
+    wait_ticks(0)
     handle.topk_int8q_async(dq, 10, s, i)
+    wait_ticks(DEFAULT_TICKS)
+    handle.topk_int8q_async(torch.from_numpy(rquery).cuda(), 10, s, i)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(i.cpu().numpy(), ref_i)
-    assert handle.fused_giveups() == 8
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    assert handle.fused_giveups() == 12
 
 
 def test_sdk_search_raises_when_the_selection_gave_up(gpu, wait_ticks):
