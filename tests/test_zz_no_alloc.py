@@ -2,7 +2,8 @@
 top-k equals msim_int4_topk_int8q_async's bit for bit, and the C oracle's
 stable top-k of its int8-query scores, on two calls in a row, the second with
 a smaller input, and the call allocates nothing (the handle's workspace,
-torch's allocations and the device's free memory stay as they were).
+torch's allocations and the device's free memory stay as they were).  Both
+entry points captured in a HIP graph and replayed match the oracle.
 """
 import ctypes
 
@@ -146,3 +147,55 @@ def test_noalloc_rejects_sizes_beyond_its_limits(gpu):
         check(call(torch.zeros((8, 16, 128), device="cuda"), 10))
     with pytest.raises(ValueError, match="k must be between"):
         check(call(query, 0))
+
+
+@pytest.mark.parametrize("entry", ["msim_int4_topk_int8q_noalloc", "msim_int4_topk_int8q_async"])
+def test_captured_call_replays_match_the_oracle(gpu, oracle, entry):
+    """The call captured in a HIP graph (the callers the no-alloc entry point
+    is for) and replayed six times over three queries, with an eager call
+    of the same entry point between replays: every replay and every eager
+    call equals the oracle's top-k.  The fused selection's launch counter
+    lives on the device, so replays, which the host does not see, still
+    tag each launch apart."""
+    import torch
+
+    lib, k = gpu, 10
+    handle, _, packed = _setup(2048, 8, 40, 4, 32, seed=41)
+    rng = np.random.default_rng(42)
+    queries = [torch.from_numpy(rng.standard_normal((4, 32, 128)).astype(np.float32)).cuda() for _ in range(3)]
+    expected = []
+    for q in queries:
+        exp = oracle.int4_int8q_scores(q.cpu().numpy(), packed.values, packed.doc_offsets,
+                                       token_scale=packed.token_scale, scale=float(packed.scale))
+        expected.append(oracle.topk(exp, k))
+    static_q = queries[0].clone()
+    scores = torch.empty((4, k), device="cuda")
+    ids = torch.empty((4, k), dtype=torch.int64, device="cuda")
+
+    def call(stream):
+        check(getattr(lib, entry)(handle._h, ptr(static_q), 4, 32, k, ptr(scores), ptr(ids),
+                                  _maxsim_hip._stream_ptr(stream)))
+
+    # A first call with these shapes outside the capture (workspaces, tables,
+    # the scratch array's address).
+    call(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    print(f"graph capture of {entry}", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    eager_s = torch.empty_like(scores)
+    eager_i = torch.empty_like(ids)
+    for r in range(6):
+        print(f"replay {r}", flush=True)
+        static_q.copy_(queries[r % 3])
+        graph.replay()
+        torch.cuda.synchronize()
+        ref_s, ref_i = expected[r % 3]
+        np.testing.assert_array_equal(ids.cpu().numpy(), ref_i)
+        np.testing.assert_array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+        got_s, got_i = _run(lib, entry, handle, queries[(r + 1) % 3], k, eager_s, eager_i)
+        ref_s, ref_i = expected[(r + 1) % 3]
+        np.testing.assert_array_equal(got_i, ref_i)
+        np.testing.assert_array_equal(got_s.view(np.uint32), ref_s.view(np.uint32))
