@@ -377,7 +377,6 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     if (h->tail_epoch.ptr == nullptr) {
       h->tail_epoch.ensure(256, "hipMalloc scan launch counter");
       check_hip(launch_fill_f32(h->tail_epoch.as<float>(), 64, 0.0f, stream), "zero scan launch counters");
-      h->fused_launches = 0;
     }
     const int64_t rows = std::min(batch, std::max<int64_t>(1, kScanPassRows / query_tokens));
     const size_t key_bytes = sizeof(uint64_t) * (size_t)(rows * kScanTailRow);
@@ -393,6 +392,7 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     }
     a.tail_keys = h->tail_keys.as<uint64_t>();
     a.tail_rec = h->tail_rec.as<uint64_t>();
+    a.tail_key_words = (int64_t)(h->tail_keys.cap / sizeof(uint64_t));
     a.topk_k = (int32_t)k;
     a.tail_cap = g_fused_topk == 2 ? 0 : INT32_MAX;
     a.epoch = h->tail_epoch.as<uint32_t>();
@@ -408,14 +408,6 @@ void score_quantized(msim_int4_docs* h, int64_t batch, int64_t query_tokens, flo
     if (k > 0) {
       a.top_scores = d_top_s + b0 * k;
       a.top_ids = d_top_i + b0 * k;
-    }
-    if (k > 0) {
-      // Each fused launch advances the counter by one; at a multiple of the
-      // key-tag period the key rows are zeroed first.
-      if (h->fused_launches > 0 && h->fused_launches % kScanTailKeyPeriod == 0)
-        check_hip(launch_fill_f32(h->tail_keys.as<float>(), (int64_t)(h->tail_keys.cap / 4), 0.0f, stream),
-                  "zero scan tail key rows at the key-tag period");
-      ++h->fused_launches;
     }
     check_hip(launch_int8q_scan(a, scan_epilogue(h), stream), "launch int8q scan kernel");
   }

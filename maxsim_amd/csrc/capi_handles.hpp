@@ -122,7 +122,6 @@ struct msim_int4_docs {
   // Scan with fused top-k: launch counter, key rows of kScanTailRow tagged
   // 64-bit keys and workgroup records (3 x kScanTailBlocks tagged words per row).
   msim::DeviceBuffer tail_epoch, tail_keys, tail_rec;
-  uint64_t fused_launches = 0;  // launches on tail_epoch so far (the device counter's value)
   msim::ScoreWorkspace ws;
 
   uint64_t resident_bytes() const {

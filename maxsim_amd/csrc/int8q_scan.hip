@@ -668,6 +668,15 @@ __global__ __launch_bounds__(kScanThreads) MSIM_SCAN_OCCUPANCY void int8q_scan_k
       __hip_atomic_store(p.epoch, tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  // Key tags repeat every kTailTagMask launches, so launches whose key tags
+  // collide are a multiple of it apart, and a launch whose tag is
+  // kTailTagMask - 1 modulo it lies between them: that launch zeroes every
+  // key row once the selection's waves are done with them.
+  if (tag % kTailTagMask == kTailTagMask - 1u) {
+    __syncthreads();
+    for (int64_t w = threadIdx.x; w < p.tail_key_words; w += kScanThreads)
+      __hip_atomic_store(p.tail_keys + w, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <int EPI, bool kTail, bool kSign>
@@ -710,7 +719,8 @@ hipError_t launch_int8q_scan(const ScanArgs& args, int epilogue, hipStream_t str
        args.num_docs < kScanTailMinDocs || args.batch > kScanTailMaxRows ||
        args.num_waves > (int64_t)kScanWaves * kScanTailBlocks || args.epoch == nullptr ||
        args.top_scores == nullptr || args.top_ids == nullptr || args.tail_keys == nullptr ||
-       args.tail_rec == nullptr || args.block_pos == nullptr))
+       args.tail_rec == nullptr || args.block_pos == nullptr ||
+       args.tail_key_words < (int64_t)args.batch * kScanTailRow))
     return hipErrorInvalidValue;
   const int nt = (rows + 15) / 16;
   const int64_t blocks = args.num_waves / kScanWaves;

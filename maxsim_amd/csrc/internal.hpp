@@ -127,6 +127,7 @@ struct ScanArgs {
   uint64_t* tail_keys;
   uint64_t* tail_rec;
   const int64_t* block_pos;
+  int64_t tail_key_words;       // u64 words of the tail_keys allocation (>= batch * kScanTailRow)
 };
 constexpr int kScanTailMaxK = 32;
 constexpr int64_t kScanTailMaxDocs = 4096;
@@ -136,9 +137,11 @@ constexpr int kScanTailMaxRows = 8;  // batch rows of one pass (two per wave)
 constexpr int kScanTailBlocks = 512;  // workgroups of a fused launch at most
 constexpr uint64_t kScanTailWaitTicks = 10000000;  // default wait of the fused selection: 100 ms
 // Launch tags repeat in the 19 tag bits of a key every kScanTailKeyPeriod
-// launches of one launch counter (tag % period + 1): the host zeroes the key
-// rows before every launch whose number is a multiple of the period, so a
-// key that carries the current tag was stored by the current launch.
+// launches of one launch counter (tag % period + 1): workgroup 0 of every
+// launch whose tag is period - 1 modulo the period zeroes all tail_key_words
+// after its selection, so a key that carries the current tag was stored by
+// the current launch.  The device does it, so replays of a captured call,
+// which the host does not see, are covered too.
 constexpr uint64_t kScanTailKeyPeriod = (1u << 19) - 1u;
 // Epilogue forms of the scan (the token scales decide which is exact):
 //  * kScanEpiIntMax: tensor-scale corpora (token_scale16 == nullptr): integer

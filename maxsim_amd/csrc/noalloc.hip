@@ -40,7 +40,6 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 unsigned char* g_scratch_ptr[kMaxDevices] = {};
-uint64_t g_fused_launches[kMaxDevices] = {};  // fused launches on each device's counter so far
 
 // Device address of this device's `scratch`, looked up at the first call on
 // the device.
@@ -104,6 +103,7 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
     if (fused) {
       a.tail_keys = reinterpret_cast<uint64_t*>(base + kKeysOff);
       a.tail_rec = reinterpret_cast<uint64_t*>(base + kRecOff);
+      a.tail_key_words = kScanTailMaxRows * kScanTailRow;
       a.topk_k = (int32_t)k;
       a.tail_cap = mode == 2 ? 0 : INT32_MAX;
       a.epoch = reinterpret_cast<uint32_t*>(base + kEpochOff);
@@ -112,20 +112,6 @@ extern "C" int msim_int4_topk_int8q_noalloc(msim_int4_docs* h, const float* d_qu
       a.top_ids = d_indices;
     }
     if (!fused) a.scores = scores;
-    if (fused) {
-      // The counter advances by one per fused launch; at a multiple of the
-      // key-tag period the key rows are zeroed first (a fill kernel, not a
-      // memset, so that a captured call records no memset node).
-      uint64_t launches;
-      {
-        std::lock_guard<std::mutex> lock(g_scratch_mutex);
-        launches = g_fused_launches[h->device]++;
-      }
-      if (launches > 0 && launches % kScanTailKeyPeriod == 0)
-        check_hip(launch_fill_f32(reinterpret_cast<float*>(base + kKeysOff),
-                                  (int64_t)(kScanTailMaxRows * kScanTailRow * 2), 0.0f, s),
-                  "zero scan tail key rows at the key-tag period");
-    }
     check_hip(launch_int8q_scan(a, scan_epilogue(h), s), "launch int8q scan kernel");
     if (!fused)
       check_hip(launch_topk(scores, batch, n, n, k, nullptr, d_scores, d_indices, s),

@@ -456,7 +456,7 @@ constexpr int kTailBlockKeys = 16;                          // documents per dee
 constexpr int kTailMaxDocs = 4096;                          // ids below 2^12
 constexpr int kTailTagBits = 19;
 constexpr uint32_t kTailTagMask = (1u << kTailTagBits) - 1u;
-static_assert(kTailTagMask == kScanTailKeyPeriod, "the host refreshes the key rows at the key-tag period");
+static_assert(kTailTagMask == kScanTailKeyPeriod, "the scan zeroes the key rows at the key-tag period");
 // LDS of the selecting wave: candidates (at most kTailCandMax, then eight
 // zero keys, then a spare slot for the stores of lanes without a
 // candidate), then the list of deep blocks (kTailHotMax entries and a spare).

@@ -199,3 +199,51 @@ def test_captured_call_replays_match_the_oracle(gpu, oracle, entry):
         ref_s, ref_i = expected[(r + 1) % 3]
         np.testing.assert_array_equal(got_i, ref_i)
         np.testing.assert_array_equal(got_s.view(np.uint32), ref_s.view(np.uint32))
+
+
+def test_replays_across_the_key_tag_period(gpu, oracle):
+    """More than 2^19 - 1 fused launches on the device's counter (1,025
+    replays of a graph of 512 captured no-alloc calls): the launch whose tag
+    closes the key-tag period zeroes the key rows on the device, and the
+    replays and calls after it stay exact."""
+    import torch
+
+    lib, k = gpu, 5
+    handle, query, packed = _setup(300, 1, 6, 2, 8, seed=51)
+    rng = np.random.default_rng(52)
+    others = [torch.from_numpy(rng.standard_normal((2, 8, 128)).astype(np.float32)).cuda() for _ in range(2)]
+
+    def expect(q):
+        exp = oracle.int4_int8q_scores(q.cpu().numpy(), packed.values, packed.doc_offsets,
+                                       token_scale=packed.token_scale, scale=float(packed.scale))
+        return oracle.topk(exp, k)
+
+    scores = torch.empty((2, k), device="cuda")
+    ids = torch.empty((2, k), dtype=torch.int64, device="cuda")
+
+    def call(stream):
+        check(lib.msim_int4_topk_int8q_noalloc(handle._h, ptr(query), 2, 8, k, ptr(scores), ptr(ids),
+                                               _maxsim_hip._stream_ptr(stream)))
+
+    call(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(512):
+            call(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for r in range(1025):
+        graph.replay()
+        if r % 256 == 255:
+            torch.cuda.synchronize()
+            print(f"replays {r + 1} ({(r + 1) * 512} launches)", flush=True)
+    torch.cuda.synchronize()
+    ref_s, ref_i = expect(query)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_i)
+    np.testing.assert_array_equal(scores.cpu().numpy().view(np.uint32), ref_s.view(np.uint32))
+    for q in others:
+        ref_s, ref_i = expect(q)
+        for entry in ("msim_int4_topk_int8q_noalloc", "msim_int4_topk_int8q_async"):
+            got_s, got_i = _run(lib, entry, handle, q, k, scores, ids)
+            np.testing.assert_array_equal(got_i, ref_i)
+            np.testing.assert_array_equal(got_s.view(np.uint32), ref_s.view(np.uint32))
